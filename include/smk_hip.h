@@ -1,0 +1,147 @@
+/*
+ * smk_hip.h -- C ABI of libsmk_hip.so, the MI355X (gfx950) decode-GEMV library.
+ *
+ * Drop-in boundary for the reference's kernel table (Mattral/simd-ml-kernels 0.3.0,
+ * src/dispatch/kernels.hpp:39-78).  Each host-pointer entry point below has the
+ * argument list of the KernelTable slot it replaces, plus an int status return:
+ * the reference's table functions return void and never fail for data; here a
+ * device error (no GPU, out of memory, launch failure) is reported as a status
+ * and smk_last_error() holds the message.  Data semantics are unchanged: a
+ * non-finite x gives an all-NaN y, K == 0 gives zeros, N == 0 writes nothing.
+ *
+ * Host-pointer calls copy x in and y out and run on the calling thread's own
+ * stream; they return after y is written.  Weights (Wq, B) are uploaded on every
+ * call unless their host range was pinned with smk_weights_pin, which keeps one
+ * device copy that later calls on any pointer inside that range reuse.
+ *
+ * smk_d_* entry points take DEVICE pointers and a hipStream_t (as void*; NULL is
+ * the null stream), only enqueue work, and never allocate.  Their buffers must
+ * be 4-byte aligned; the fast paths also want 16-byte aligned rows.
+ *
+ * No torch or Python types cross this boundary.
+ */
+#ifndef SMK_HIP_H
+#define SMK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define SMK_OK 0
+#define SMK_ERR_ARGUMENT 1      /* invalid shape / pointer / option */
+#define SMK_ERR_NO_DEVICE 2     /* no usable gfx950 device */
+#define SMK_ERR_DEVICE 3        /* a HIP call failed */
+#define SMK_ERR_OUT_OF_MEMORY 4 /* device or pinned allocation failed */
+#define SMK_ERR_DATA 5          /* quantizer input not finite, or a block scale overflows float16 */
+
+/* Message of the calling thread's last failure ("" after success). */
+const char* smk_last_error(void);
+/* Library version string. */
+const char* smk_version(void);
+/* Device name, arch (e.g. "gfx950"), CU count and HBM bytes of the device in use. */
+int smk_device_info(char* name, size_t name_len, char* arch, size_t arch_len, int* compute_units,
+                    size_t* hbm_bytes);
+
+/* ─── Host-pointer entry points (KernelTable slots) ───────────────────────── */
+
+/* KernelTable::gemv_q4_0, GemvQ4_0Fn (kernels.hpp:52-53, q4_0.hpp:63-72):
+ * y[n] = sum_k x[k] W[n][k], W as N*(K/32) GGUF Q4_0 blocks of 18 bytes, K % 32 == 0. */
+int smk_gemv_q4_0(int N, int K, const float* x, const uint8_t* Wq, float* y);
+/* KernelTable::gemv_q8_0, GemvQ8_0Fn (kernels.hpp:50-51, q8_0.hpp:171-178): 34-byte Q8_0 blocks. */
+int smk_gemv_q8_0(int N, int K, const float* x, const uint8_t* Wq, float* y);
+/* KernelTable::sgemm, SgemmFn (kernels.hpp:38-41): C = alpha op(A) op(B) + beta C, FP32. */
+int smk_sgemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, int lda, const float* B,
+              int ldb, float beta, float* C, int ldc);
+/* KernelTable::sgemm_f16, Sgemm16Fn (kernels.hpp:42-45, f16_gemm.hpp:37-44): binary16 A and B,
+ * FP32 accumulation and C; trans_b: B stored N x K (x W^T). */
+int smk_sgemm_f16(int trans_b, int M, int N, int K, float alpha, const uint16_t* A, int lda, const uint16_t* B,
+                  int ldb, float beta, float* C, int ldc);
+/* KernelTable::sgemm_bf16, Sgemm16Fn (kernels.hpp:42-45, bf16_gemm.hpp:40-47): BF16 bit patterns. */
+int smk_sgemm_bf16(int trans_b, int M, int N, int K, float alpha, const uint16_t* A, int lda, const uint16_t* B,
+                   int ldb, float beta, float* C, int ldc);
+/* KernelTable::silu, RowFn (kernels.hpp:55, activations.hpp:18-23): out = x / (1 + exp(-x)). */
+int smk_silu(const float* in, float* out, int n);
+/* KernelTable::softmax_row, RowFn (kernels.hpp:55, activations.hpp:25-28), over `rows` rows of n. */
+int smk_softmax(const float* in, float* out, int rows, int n);
+/* quantize_q4_0_rows (q4_0.hpp:54-60): W [N, K] -> GGUF Q4_0 blocks; SMK_ERR_DATA on rejection. */
+int smk_quantize_q4_0(const float* W, int N, int K, uint8_t* out);
+/* quantize_q8_0_rows (q8_0.hpp:136-142): W [N, K] -> GGUF Q8_0 blocks; SMK_ERR_DATA on rejection. */
+int smk_quantize_q8_0(const float* W, int N, int K, uint8_t* out);
+
+/* No reference counterpart (the reference computes these in numpy, examples/llama/llama.py:184-187
+ * and :169-178 / :387-396): RMSNorm over `rows` rows of n, and RoPE of x [heads, head_dim] with the
+ * cos/sin of one position ([head_dim], halves equal); interleaved != 0 rotates pairs (2i, 2i+1). */
+int smk_rms_norm(const float* x, const float* weight, float* y, int rows, int n, double eps);
+int smk_rope(const float* x, const float* cos, const float* sin, float* y, int heads, int head_dim,
+             int interleaved);
+/* No reference counterpart (the reference has no batched Q4_0/Q8_0 API, pybind_entry.cpp:956-957):
+ * Y [M, N] = X [M, K] W^T, each row of X quantized to Q8 independently (row m equals gemv(X[m])). */
+int smk_gemm_q4_0(int M, int N, int K, const float* X, const uint8_t* Wq, float* Y);
+int smk_gemm_q8_0(int M, int N, int K, const float* X, const uint8_t* Wq, float* Y);
+
+/* Device-resident weights, keyed by host address range (new: the reference reads host memory). */
+int smk_weights_pin(const void* host, size_t nbytes);
+int smk_weights_unpin(const void* host);
+int smk_weights_stats(size_t* bytes, int* entries);
+
+/* ─── Device-pointer entry points (async on `stream`) ─────────────────────── */
+int smk_d_gemv_q4_0(int N, int K, const float* x, const uint8_t* Wq, float* y, void* stream);
+int smk_d_gemv_q8_0(int N, int K, const float* x, const uint8_t* Wq, float* y, void* stream);
+/* Rows m < M (M <= 8) of X [M, ldx] against the same W: Y [M, ldy]. */
+int smk_d_gemm_q4_0(int M, int N, int K, const float* X, int ldx, const uint8_t* Wq, float* Y, int ldy, void* stream);
+int smk_d_gemm_q8_0(int M, int N, int K, const float* X, int ldx, const uint8_t* Wq, float* Y, int ldy, void* stream);
+/* elem: 0 FP32, 1 FP16, 2 BF16.  C = beta C + alpha A B^T, A [M, lda], B [N, ldb]. */
+int smk_d_gemm_tb(int elem, int M, int N, int K, float alpha, const void* A, int lda, const void* B, int ldb,
+                  float beta, float* C, int ldc, void* stream);
+int smk_d_sgemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, int lda, const float* B,
+                int ldb, float beta, float* C, int ldc, void* stream);
+int smk_d_silu(const float* in, float* out, long long n, void* stream);
+int smk_d_softmax(const float* in, float* out, int rows, int n, void* stream);
+int smk_d_rms_norm(const float* x, const float* weight, float* y, int rows, int n, double eps, void* stream);
+int smk_d_rope(const float* x, const float* cos, const float* sin, float* y, int heads, int head_dim, int interleaved,
+               void* stream);
+/* block_bytes 18 (Q4_0) or 34 (Q8_0).  bad: device int set to 1 on rejection (caller zeroes it). */
+int smk_d_quantize(int block_bytes, long long rows, int K, const float* W, uint8_t* out, int* bad, void* stream);
+/* Parity helpers: x's Q8 quants/scales (bad as above) and per-block int32 sums [N, K/32]. */
+int smk_d_quantize_x_q8(int K, const float* x, int8_t* qs, float* dx, int* bad, void* stream);
+int smk_d_block_sums(int block_bytes, int N, int K, const int8_t* qs, const uint8_t* Wq, int32_t* out, void* stream);
+/* HBM read roof: streams nbytes from src (16-byte aligned); sink: >= 2048 floats, never read back. */
+int smk_d_read_roof(const void* src, size_t nbytes, float* sink, void* stream);
+
+/* Device memory, copies, streams, events and graphs, for callers without their own runtime
+ * objects (the tests and bench.py use these; no other framework is loaded with the library). */
+int smk_malloc(void** dptr, size_t nbytes);
+int smk_free(void* dptr);
+int smk_memcpy_h2d(void* dst, const void* src, size_t nbytes);
+int smk_memcpy_d2h(void* dst, const void* src, size_t nbytes);
+int smk_memcpy_d2d(void* dst, const void* src, size_t nbytes);
+int smk_memset(void* dptr, int byte, size_t nbytes);
+int smk_synchronize(void);
+int smk_stream_create(void** stream);
+int smk_stream_destroy(void* stream);
+int smk_stream_synchronize(void* stream);
+int smk_event_create(void** event);
+int smk_event_destroy(void* event);
+int smk_event_record(void* event, void* stream);
+int smk_event_elapsed_ms(void* start, void* end, float* ms);
+/* Capture the work enqueued on `stream` between begin and end into an executable graph. */
+int smk_graph_begin(void* stream);
+int smk_graph_end(void* stream, void** graph_exec);
+int smk_graph_launch(void* graph_exec, void* stream);
+int smk_graph_destroy(void* graph_exec);
+/* HIP runtime version in use and the one the library was built against (HIP_VERSION). */
+int smk_runtime_version(int* runtime, int* built);
+
+/* Diagnostics: force the quantized GEMV's lanes per row / rows per workgroup (0 = automatic),
+ * and report the kernel a call would use ("pairs" or "generic"). */
+int smk_set_gemv_tuning(int lanes_per_row, int rows_per_wg);
+const char* smk_gemv_path(int K, const void* Wq);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

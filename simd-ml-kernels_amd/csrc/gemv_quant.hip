@@ -1,0 +1,529 @@
+// gemv_quant.hip -- decode GEMV y = x * W^T on GGUF Q4_0 / Q8_0 blocks, for gfx950.
+//
+// Semantics are those of the reference's gemv_q4_0 / gemv_q8_0 (q4_0.hpp:23-33,
+// q8_0.hpp:101-112, driver q8_0_scalar.cpp:315-361): x is quantized once to Q8 blocks
+// (int8 quants, FP32 scales dx = amax/127), every 32-term block product is an exact
+// int32, and y[n] = sum_b fp16(dw[n][b]) * dx[b] * isum[n][b] in FP32.
+//
+// Layout in HBM: W is read exactly as GGUF stores it, N rows of K/32 blocks (18 or 34
+// bytes each), never repacked.  Two consecutive blocks form a 36- or 68-byte "pair"
+// that always starts on a 4-byte boundary, so a lane streams whole pairs with 16-byte
+// loads (dwordx4, 4-byte aligned) and v_alignbyte moves the block-A bytes past the
+// 2-byte scale.  Each W byte is read once; x (K floats) is re-read by every workgroup
+// from L2.
+//
+// Per workgroup (256 threads = 4 waves):
+//   1. issue the first pair loads of W (so HBM latency overlaps step 2),
+//   2. quantize x into LDS, bit-exact with quantize_x_q8 (q8_0_scalar.cpp:237-256,
+//      308-313): IEEE amax/127 and 1/d, product and rounding as separate operations,
+//      ties away from zero.  Q4_0 also stores -8 * sum(qx) per block, the starting
+//      value of the block's dot so that sum((q-8)*qx) = sum(q*qx) - 8*sum(qx)
+//      (the identity of q4_0_rows.hpp:25-31),
+//   3. each wave walks its rows of W: LPR lanes share a row, a lane owns pairs
+//      j, j+LPR, ...; v_dot4_i32_i8 does the 32-term integer sums; one fmaf per block
+//      adds isum * (dw * dx) into the lane's FP32 partial; a shuffle tree sums the
+//      LPR partials.  Loads for the next step are issued before the current step's
+//      arithmetic (two register buffers).
+//
+// LDS layout of the x quants (pair kernel): four planes of uint4 per row of x,
+// plane q holds, for every pair p, the 16 quants that multiply 16 W bytes of that
+// pair: q=0 block 2p values 0-15, q=1 block 2p values 16-31, q=2/3 block 2p+1.
+// Lanes j, j+1, ... read consecutive 16-byte entries of a plane: no bank conflicts.
+#include "device_common.hpp"
+#include "launch.hpp"
+
+#include <algorithm>
+
+namespace smk {
+namespace {
+
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+constexpr int kThreads = 256;
+
+// ─── x -> Q8 quants in LDS ───────────────────────────────────────────────────
+
+// Destination dword of quant dword k (values 4k..4k+3) of block b.
+template <bool kPlanes>
+__device__ __forceinline__ int x_dword_index(int b, int k, int pairs) {
+    if (!kPlanes) return 8 * b + k;
+    const int p = b >> 1, q = 2 * (b & 1) + (k >> 2);
+    return 4 * (q * pairs + p) + (k & 3);
+}
+
+// Rows m < M of x ([M, ldx] floats) into lds_q ([M][K/4] dwords), lds_bias ([M][nb], Q4_0:
+// -8 * sum of the block's quants) and lds_dx ([M][nb]); bad[m] = 1 if row m is not finite.
+// 8 consecutive threads hold one 32-value block, 4 values each.
+template <bool kPlanes, bool kBias>
+__device__ void quantize_x_into_lds(const float* __restrict__ x, int ldx, int M, int K, uint32_t* lds_q,
+                                    int* lds_bias, float* lds_dx, int* bad) {
+    const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
+    const int total = M * quads;
+    for (int qd = threadIdx.x; qd < total; qd += blockDim.x) {
+        const int m = qd / quads;
+        const int kq = qd - m * quads;
+        const int b = kq >> 3, k = kq & 7;
+        const float* src = x + static_cast<size_t>(m) * ldx + 4 * kq;
+        const float v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
+        const bool fin = (finite_bits(v0) & finite_bits(v1) & finite_bits(v2) & finite_bits(v3)) != 0;
+        float amax = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+        amax = group_max<8>(amax);
+        const float d = amax / 127.0f;                 // IEEE division (correctly rounded)
+        float id = d != 0.0f ? 1.0f / d : 0.0f;
+        if (!(id <= 3.40282347e38f)) id = 0.0f;        // 1/d overflows: q = 0 (q8_0_scalar.cpp:249-252)
+        int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+        if (fin) {
+            q0 = round_half_away(v0 * id);
+            q1 = round_half_away(v1 * id);
+            q2 = round_half_away(v2 * id);
+            q3 = round_half_away(v3 * id);
+        }
+        const uint32_t packed = (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8) |
+                                ((static_cast<uint32_t>(q2) & 0xffu) << 16) | (static_cast<uint32_t>(q3) << 24);
+        lds_q[m * quads + x_dword_index<kPlanes>(b, k, pairs)] = packed;
+        if (kBias) {
+            const int s = group_sum_int<8>(q0 + q1 + q2 + q3);
+            if (k == 0) lds_bias[m * nb + b] = -8 * s;
+        }
+        if (k == 0) lds_dx[m * nb + b] = d;
+        if (!fin) bad[m] = 1;
+    }
+}
+
+// ─── the pair kernel (K/32 even, W 4-byte aligned) ──────────────────────────
+
+template <int BB>
+struct PairTraits;
+template <>
+struct PairTraits<kQ4_0Bytes> {
+    static constexpr int kDwords = 9;  // 36 bytes
+    static constexpr bool kBias = true;
+};
+template <>
+struct PairTraits<kQ8_0Bytes> {
+    static constexpr int kDwords = 17;  // 68 bytes
+    static constexpr bool kBias = false;
+};
+
+template <int D>
+__device__ __forceinline__ void load_pair(const uint8_t* src, uint32_t (&w)[D]) {
+    const u32x4a4* v = reinterpret_cast<const u32x4a4*>(src);
+#pragma unroll
+    for (int i = 0; i < D / 4; ++i) {
+        const u32x4a4 t = __builtin_nontemporal_load(v + i);
+        w[4 * i + 0] = t.x;
+        w[4 * i + 1] = t.y;
+        w[4 * i + 2] = t.z;
+        w[4 * i + 3] = t.w;
+    }
+    w[D - 1] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src) + (D - 1));
+}
+
+// Integer sums of one pair: sA for block 2p, sB for block 2p+1.  xq[0..3]: the four planes.
+__device__ __forceinline__ void pair_isums(const uint32_t (&w)[9], const uint4 (&xq)[4], int biasA, int biasB,
+                                           int& sA, int& sB) {
+    constexpr uint32_t lo4 = 0x0f0f0f0fu;
+    // Block A: scale in bytes 0-1, nibbles in bytes 2-17.
+    const uint32_t a0 = skip2(w[1], w[0]), a1 = skip2(w[2], w[1]), a2 = skip2(w[3], w[2]), a3 = skip2(w[4], w[3]);
+    int s = biasA;
+    s = dot4(a0 & lo4, xq[0].x, s);
+    s = dot4(a1 & lo4, xq[0].y, s);
+    s = dot4(a2 & lo4, xq[0].z, s);
+    s = dot4(a3 & lo4, xq[0].w, s);
+    s = dot4((a0 >> 4) & lo4, xq[1].x, s);
+    s = dot4((a1 >> 4) & lo4, xq[1].y, s);
+    s = dot4((a2 >> 4) & lo4, xq[1].z, s);
+    s = dot4((a3 >> 4) & lo4, xq[1].w, s);
+    sA = s;
+    // Block B: scale in bytes 18-19 (high half of w[4]), nibbles in w[5..8].
+    s = biasB;
+    s = dot4(w[5] & lo4, xq[2].x, s);
+    s = dot4(w[6] & lo4, xq[2].y, s);
+    s = dot4(w[7] & lo4, xq[2].z, s);
+    s = dot4(w[8] & lo4, xq[2].w, s);
+    s = dot4((w[5] >> 4) & lo4, xq[3].x, s);
+    s = dot4((w[6] >> 4) & lo4, xq[3].y, s);
+    s = dot4((w[7] >> 4) & lo4, xq[3].z, s);
+    s = dot4((w[8] >> 4) & lo4, xq[3].w, s);
+    sB = s;
+}
+
+__device__ __forceinline__ void pair_isums(const uint32_t (&w)[17], const uint4 (&xq)[4], int, int, int& sA,
+                                           int& sB) {
+    // Block A: scale bytes 0-1, quants bytes 2-33; block B: scale bytes 34-35, quants 36-67.
+    int s = 0;
+    s = dot4(skip2(w[1], w[0]), xq[0].x, s);
+    s = dot4(skip2(w[2], w[1]), xq[0].y, s);
+    s = dot4(skip2(w[3], w[2]), xq[0].z, s);
+    s = dot4(skip2(w[4], w[3]), xq[0].w, s);
+    s = dot4(skip2(w[5], w[4]), xq[1].x, s);
+    s = dot4(skip2(w[6], w[5]), xq[1].y, s);
+    s = dot4(skip2(w[7], w[6]), xq[1].z, s);
+    s = dot4(skip2(w[8], w[7]), xq[1].w, s);
+    sA = s;
+    s = 0;
+    s = dot4(w[9], xq[2].x, s);
+    s = dot4(w[10], xq[2].y, s);
+    s = dot4(w[11], xq[2].z, s);
+    s = dot4(w[12], xq[2].w, s);
+    s = dot4(w[13], xq[3].x, s);
+    s = dot4(w[14], xq[3].y, s);
+    s = dot4(w[15], xq[3].z, s);
+    s = dot4(w[16], xq[3].w, s);
+    sB = s;
+}
+
+template <int D>
+__device__ __forceinline__ float scale_a(const uint32_t (&w)[D]) { return half_bits_to_float(w[0]); }
+template <int D>
+__device__ __forceinline__ float scale_b(const uint32_t (&w)[D]) { return half_bits_to_float(w[D / 2] >> 16); }
+
+// BB: block bytes; LPR: lanes per row; U: rows per lane group in one step; MT: max rows of x.
+template <int BB, int LPR, int U, int MT>
+__global__ __launch_bounds__(kThreads) void gemv_pairs_kernel(int M, int N, int K, const float* __restrict__ x,
+                                                              int ldx, const uint8_t* __restrict__ W,
+                                                              float* __restrict__ y, int ldy, int rows_per_wg) {
+    using T = PairTraits<BB>;
+    constexpr int D = T::kDwords;
+    constexpr int G = kWave / LPR;           // rows side by side in one wave
+    constexpr int kRowsPerIter = 4 * G * U;  // rows one workgroup step covers
+    extern __shared__ __align__(16) uint32_t lds[];
+    __shared__ int bad[MT];
+
+    const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
+    const size_t row_bytes = static_cast<size_t>(nb) * BB;
+    uint32_t* lds_q = lds;
+    int* lds_bias = reinterpret_cast<int*>(lds + M * quads);
+    float* lds_dx = reinterpret_cast<float*>(lds_bias + M * nb);
+
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int g = lane / LPR, j = lane % LPR;
+    const int row0 = blockIdx.x * rows_per_wg;
+    const int row_end = min(N, row0 + rows_per_wg);
+    const int chunks = (pairs + LPR - 1) / LPR;
+    const int iters = (row_end - row0 + kRowsPerIter - 1) / kRowsPerIter;
+    const int steps = iters * chunks;
+
+    if (threadIdx.x < MT) bad[threadIdx.x] = 0;
+
+    auto load_step = [&](int s, uint32_t (&w)[U][D]) {
+        const int it = s / chunks, c = s - it * chunks;
+        const int p = j + c * LPR;
+        const int rb = row0 + it * kRowsPerIter + (wave * U) * G + g;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int r = rb + u * G;
+            if (r < row_end && p < pairs) load_pair<D>(W + r * row_bytes + static_cast<size_t>(p) * (2 * BB), w[u]);
+        }
+    };
+
+    uint32_t wa[U][D], wb[U][D];
+    if (steps > 0) load_step(0, wa);
+    __syncthreads();  // bad[] cleared
+    quantize_x_into_lds<true, T::kBias>(x, ldx, M, K, lds_q, lds_bias, lds_dx, bad);
+    __syncthreads();
+
+    float acc[U][MT];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[u][m] = 0.0f;
+
+    auto body = [&](int s, uint32_t (&cur)[U][D], uint32_t (&nxt)[U][D]) {
+        if (s + 1 < steps) load_step(s + 1, nxt);
+        const int it = s / chunks, c = s - it * chunks;
+        const int p = j + c * LPR;
+        if (p < pairs) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (m < M) {
+                    const uint4* planes = reinterpret_cast<const uint4*>(lds_q + m * quads);
+                    const uint4 xq[4] = {planes[p], planes[pairs + p], planes[2 * pairs + p], planes[3 * pairs + p]};
+                    const int biasA = T::kBias ? lds_bias[m * nb + 2 * p] : 0;
+                    const int biasB = T::kBias ? lds_bias[m * nb + 2 * p + 1] : 0;
+                    const float dxA = lds_dx[m * nb + 2 * p], dxB = lds_dx[m * nb + 2 * p + 1];
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        int sA, sB;
+                        pair_isums(cur[u], xq, biasA, biasB, sA, sB);
+                        const float scA = scale_a(cur[u]) * dxA;
+                        const float scB = scale_b(cur[u]) * dxB;
+                        acc[u][m] = fmaf(static_cast<float>(sA), scA, acc[u][m]);
+                        acc[u][m] = fmaf(static_cast<float>(sB), scB, acc[u][m]);
+                    }
+                }
+            }
+        }
+        if (c == chunks - 1) {
+            const int rb = row0 + it * kRowsPerIter + (wave * U) * G + g;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const float tot = group_sum<LPR>(acc[u][m]);
+                    acc[u][m] = 0.0f;
+                    const int r = rb + u * G;
+                    if (m < M && j == 0 && r < row_end) y[static_cast<size_t>(m) * ldy + r] = bad[m] ? __builtin_nanf("") : tot;
+                }
+            }
+        }
+    };
+
+    int s = 0;
+    for (; s + 1 < steps; s += 2) {
+        body(s, wa, wb);
+        body(s + 1, wb, wa);
+    }
+    if (s < steps) body(s, wa, wb);
+}
+
+// ─── the generic kernel (any K/32, W 2-byte aligned) ─────────────────────────
+// One wave per row, lanes over blocks; 16-bit loads.  Used for odd K/32 only.
+template <int BB, int MT>
+__global__ __launch_bounds__(kThreads) void gemv_generic_kernel(int M, int N, int K, const float* __restrict__ x,
+                                                                int ldx, const uint8_t* __restrict__ W,
+                                                                float* __restrict__ y, int ldy, int rows_per_wg) {
+    constexpr bool kQ4 = BB == kQ4_0Bytes;
+    extern __shared__ __align__(16) uint32_t lds[];
+    __shared__ int bad[MT];
+    const int nb = K >> 5, quads = K >> 2;
+    uint32_t* lds_q = lds;
+    int* lds_bias = reinterpret_cast<int*>(lds + M * quads);
+    float* lds_dx = reinterpret_cast<float*>(lds_bias + M * nb);
+    if (threadIdx.x < MT) bad[threadIdx.x] = 0;
+    __syncthreads();
+    quantize_x_into_lds<false, kQ4>(x, ldx, M, K, lds_q, lds_bias, lds_dx, bad);
+    __syncthreads();
+
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int row0 = blockIdx.x * rows_per_wg;
+    const int row_end = min(N, row0 + rows_per_wg);
+    for (int r = row0 + wave; r < row_end; r += kThreads / kWave) {
+        float acc[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+        for (int b = lane; b < nb; b += kWave) {
+            const uint16_t* h = reinterpret_cast<const uint16_t*>(W + (static_cast<size_t>(r) * nb + b) * BB);
+            const float dw = half_bits_to_float(h[0]);
+            uint32_t q[8];
+#pragma unroll
+            for (int k = 0; k < (kQ4 ? 4 : 8); ++k)
+                q[k] = static_cast<uint32_t>(h[1 + 2 * k]) | (static_cast<uint32_t>(h[2 + 2 * k]) << 16);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (m >= M) continue;
+                const uint32_t* xq = lds_q + m * quads + 8 * b;
+                int s = kQ4 ? lds_bias[m * nb + b] : 0;
+                if (kQ4) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        s = dot4(q[k] & 0x0f0f0f0fu, xq[k], s);
+                        s = dot4((q[k] >> 4) & 0x0f0f0f0fu, xq[4 + k], s);
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) s = dot4(q[k], xq[k], s);
+                }
+                acc[m] = fmaf(static_cast<float>(s), dw * lds_dx[m * nb + b], acc[m]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const float tot = group_sum<kWave>(acc[m]);
+            if (m < M && lane == 0) y[static_cast<size_t>(m) * ldy + r] = bad[m] ? __builtin_nanf("") : tot;
+        }
+    }
+}
+
+__global__ void fill_kernel(float* y, long long n, float v) {
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<long long>(gridDim.x) * blockDim.x)
+        y[i] = v;
+}
+
+// ─── standalone x quantization and block sums (parity entry points) ─────────
+
+__global__ __launch_bounds__(kThreads) void quantize_x_kernel(int K, const float* __restrict__ x,
+                                                              int8_t* __restrict__ qs, float* __restrict__ dx,
+                                                              int* __restrict__ bad) {
+    // One workgroup per 32 blocks: reuse the LDS routine on a slice of x, then copy out.
+    extern __shared__ __align__(16) uint32_t lds[];
+    __shared__ int bad1[1];
+    const int nb_all = K >> 5;
+    const int b0 = blockIdx.x * 32;
+    const int nbk = min(32, nb_all - b0);
+    const int Kk = nbk * 32;
+    if (threadIdx.x == 0) bad1[0] = 0;
+    __syncthreads();
+    int* lds_bias = reinterpret_cast<int*>(lds + (Kk >> 2));
+    float* lds_dx = reinterpret_cast<float*>(lds_bias + nbk);
+    quantize_x_into_lds<false, false>(x + 32 * b0, Kk, 1, Kk, lds, lds_bias, lds_dx, bad1);
+    __syncthreads();
+    for (int i = threadIdx.x; i < (Kk >> 2); i += blockDim.x)
+        reinterpret_cast<uint32_t*>(qs + 32 * b0)[i] = lds[i];
+    for (int i = threadIdx.x; i < nbk; i += blockDim.x) dx[b0 + i] = lds_dx[i];
+    if (threadIdx.x == 0 && bad1[0]) atomicOr(bad, 1);
+}
+
+template <int BB>
+__global__ void block_sums_kernel(int N, int K, const int8_t* __restrict__ qs, const uint8_t* __restrict__ W,
+                                  int32_t* __restrict__ out) {
+    const int nb = K >> 5;
+    const long long total = static_cast<long long>(N) * nb;
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const int b = static_cast<int>(i % nb);
+        const uint8_t* blk = W + i * BB + 2;
+        const int8_t* xq = qs + 32 * b;
+        int s = 0;
+        if (BB == kQ4_0Bytes) {
+            for (int t = 0; t < 16; ++t)
+                s += (static_cast<int>(blk[t] & 0x0f) - 8) * xq[t] + (static_cast<int>(blk[t] >> 4) - 8) * xq[16 + t];
+        } else {
+            for (int t = 0; t < 32; ++t) s += static_cast<int>(static_cast<int8_t>(blk[t])) * xq[t];
+        }
+        out[i] = s;
+    }
+}
+
+// ─── host side ───────────────────────────────────────────────────────────────
+
+bool pair_path_ok(int K, const uint8_t* W) {
+    return ((K >> 5) % 2 == 0) && (reinterpret_cast<uintptr_t>(W) % 4 == 0);
+}
+
+int choose_lpr(int pairs) {
+    for (int l : {64, 32, 16, 8})
+        if (pairs % l == 0) return l;
+    int l = 8;
+    while (l < 64 && l * 2 <= pairs) l *= 2;
+    return l;
+}
+
+template <int BB, int LPR, int U, int MT>
+hipError_t launch_pairs(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
+                        int rows_per_wg, hipStream_t stream) {
+    constexpr int G = kWave / LPR;
+    constexpr int kRowsPerIter = 4 * G * U;
+    if (rows_per_wg <= 0) {
+        // About two workgroups per CU on a 256-CU MI355X, in whole workgroup steps.
+        const int want = (N + 511) / 512;
+        rows_per_wg = std::max(kRowsPerIter, (want + kRowsPerIter - 1) / kRowsPerIter * kRowsPerIter);
+    }
+    const int nb = K >> 5;
+    const size_t lds = static_cast<size_t>(M) * (K + 8 * nb);
+    const int grid = (N + rows_per_wg - 1) / rows_per_wg;
+    if (const hipError_t e = allow_lds(gemv_pairs_kernel<BB, LPR, U, MT>, lds); e != hipSuccess) return e;
+    hipLaunchKernelGGL((gemv_pairs_kernel<BB, LPR, U, MT>), dim3(grid), dim3(kThreads), lds, stream, M, N, K, x, ldx,
+                       W, y, ldy, rows_per_wg);
+    return hipGetLastError();
+}
+
+template <int BB, int MT>
+hipError_t launch_pairs_lpr(int lpr, int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y,
+                            int ldy, int rows_per_wg, hipStream_t stream) {
+    constexpr int U = BB == kQ4_0Bytes ? (MT <= 2 ? 4 : 2) : (MT <= 2 ? 2 : 1);
+    switch (lpr) {
+        case 64: return launch_pairs<BB, 64, U, MT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
+        case 32: return launch_pairs<BB, 32, U, MT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
+        case 16: return launch_pairs<BB, 16, U, MT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
+        default: return launch_pairs<BB, 8, U, MT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
+    }
+}
+
+template <int BB, int MT>
+hipError_t launch_generic(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
+                          hipStream_t stream) {
+    const int rows_per_wg = 16;
+    const int nb = K >> 5;
+    const size_t lds = static_cast<size_t>(M) * (K + 8 * nb);
+    const int grid = (N + rows_per_wg - 1) / rows_per_wg;
+    if (const hipError_t e = allow_lds(gemv_generic_kernel<BB, MT>, lds); e != hipSuccess) return e;
+    hipLaunchKernelGGL((gemv_generic_kernel<BB, MT>), dim3(grid), dim3(kThreads), lds, stream, M, N, K, x, ldx, W, y,
+                       ldy, rows_per_wg);
+    return hipGetLastError();
+}
+
+template <int BB>
+hipError_t gemv_quant_fmt(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
+                          hipStream_t stream, const GemvTuning* t) {
+    const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+    if (!pair_path_ok(K, W)) {
+        switch (mt) {
+            case 1: return launch_generic<BB, 1>(M, N, K, x, ldx, W, y, ldy, stream);
+            case 2: return launch_generic<BB, 2>(M, N, K, x, ldx, W, y, ldy, stream);
+            case 4: return launch_generic<BB, 4>(M, N, K, x, ldx, W, y, ldy, stream);
+            default: return launch_generic<BB, 8>(M, N, K, x, ldx, W, y, ldy, stream);
+        }
+    }
+    const int lpr = (t && t->lanes_per_row) ? t->lanes_per_row : choose_lpr((K >> 5) / 2);
+    const int rpw = t ? t->rows_per_wg : 0;
+    switch (mt) {
+        case 1: return launch_pairs_lpr<BB, 1>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
+        case 2: return launch_pairs_lpr<BB, 2>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
+        case 4: return launch_pairs_lpr<BB, 4>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
+        default: return launch_pairs_lpr<BB, 8>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
+    }
+}
+
+}  // namespace
+
+hipError_t fill(float* y, long long n, float value, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int grid = static_cast<int>(std::min<long long>((n + 255) / 256, 1024));
+    hipLaunchKernelGGL(fill_kernel, dim3(grid), dim3(256), 0, stream, y, n, value);
+    return hipGetLastError();
+}
+
+hipError_t gemv_quant(int block_bytes, int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y,
+                      int ldy, hipStream_t stream, const GemvTuning* tuning) {
+    if (N <= 0 || M <= 0) return hipSuccess;
+    if (M > 8 || K < 0 || K % 32 != 0) return hipErrorInvalidValue;
+    if (K == 0) {
+        for (int m = 0; m < M; ++m) {
+            const hipError_t e = fill(y + static_cast<size_t>(m) * ldy, N, 0.0f, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    if (block_bytes != kQ4_0Bytes && block_bytes != kQ8_0Bytes) return hipErrorInvalidValue;
+    // The x quants of one launch live in LDS (K + 8*K/32 bytes per row of x): split the rows of
+    // x so that each launch fits in 144 KiB of the CU's 160 KiB.
+    const size_t per_row = static_cast<size_t>(K) + 8 * static_cast<size_t>(K >> 5);
+    const int rows_fit = static_cast<int>(std::min<size_t>(8, (144 * 1024) / per_row));
+    if (rows_fit < 1) return hipErrorInvalidValue;  // K > ~117k
+    for (int m0 = 0; m0 < M; m0 += rows_fit) {
+        const int mr = std::min(rows_fit, M - m0);
+        const float* xm = x + static_cast<size_t>(m0) * ldx;
+        float* ym = y + static_cast<size_t>(m0) * ldy;
+        const hipError_t e = block_bytes == kQ4_0Bytes
+                                 ? gemv_quant_fmt<kQ4_0Bytes>(mr, N, K, xm, ldx, W, ym, ldy, stream, tuning)
+                                 : gemv_quant_fmt<kQ8_0Bytes>(mr, N, K, xm, ldx, W, ym, ldy, stream, tuning);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+const char* gemv_quant_path(int, int, int K, const uint8_t* W) { return pair_path_ok(K, W) ? "pairs" : "generic"; }
+
+hipError_t quantize_x_q8(int K, const float* x, int8_t* qs, float* dx, int* bad, hipStream_t stream) {
+    if (K <= 0) return hipSuccess;
+    const int nb = K >> 5;
+    const int grid = (nb + 31) / 32;
+    hipLaunchKernelGGL(quantize_x_kernel, dim3(grid), dim3(kThreads), 32 * 32 + 8 * 32, stream, K, x, qs, dx, bad);
+    return hipGetLastError();
+}
+
+hipError_t block_sums(int block_bytes, int N, int K, const int8_t* qs, const uint8_t* W, int32_t* out,
+                      hipStream_t stream) {
+    const long long total = static_cast<long long>(N) * (K >> 5);
+    if (total <= 0) return hipSuccess;
+    const int grid = static_cast<int>(std::min<long long>((total + 255) / 256, 4096));
+    if (block_bytes == kQ4_0Bytes)
+        hipLaunchKernelGGL(block_sums_kernel<kQ4_0Bytes>, dim3(grid), dim3(256), 0, stream, N, K, qs, W, out);
+    else
+        hipLaunchKernelGGL(block_sums_kernel<kQ8_0Bytes>, dim3(grid), dim3(256), 0, stream, N, K, qs, W, out);
+    return hipGetLastError();
+}
+
+}  // namespace smk

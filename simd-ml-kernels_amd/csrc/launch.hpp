@@ -1,0 +1,62 @@
+// launch.hpp -- internal launchers of the gfx950 kernels (device pointers, async on a stream).
+// The C ABI (smk_hip.h) is built on these; nothing here is exported.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace smk {
+
+// Block bytes of the two GGUF weight formats.
+constexpr int kQ4_0Bytes = 18;
+constexpr int kQ8_0Bytes = 34;
+
+// Tuning knobs of the quantized GEMV; zero fields take the built-in choice.
+struct GemvTuning {
+    int lanes_per_row = 0;  // 8, 16, 32 or 64 lanes share one row of W
+    int rows_per_wg = 0;    // rows of W per workgroup
+};
+
+// y[m*ldy + n] = sum_k x[m*ldx + k] * W[n][k] for m < M (M <= 8), W in GGUF Q4_0 (block_bytes 18)
+// or Q8_0 (34) blocks; each row of x is quantized to Q8 blocks inside the kernel.  A row of x
+// with a NaN or +-Inf makes its whole row of y NaN; K == 0 gives zeros.  K % 32 == 0.
+hipError_t gemv_quant(int block_bytes, int M, int N, int K, const float* x, int ldx, const uint8_t* W,
+                      float* y, int ldy, hipStream_t stream, const GemvTuning* tuning = nullptr);
+
+// The kernel gemv_quant would launch, for reports: "pairs" or "generic".
+const char* gemv_quant_path(int block_bytes, int N, int K, const uint8_t* W);
+
+// x -> Q8 quants and FP32 scales on the device (qs int8 [K], dx float [K/32]); *bad = 1 when x
+// holds a NaN or +-Inf.  Bit-exact with the reference's quantize_x_q8.
+hipError_t quantize_x_q8(int K, const float* x, int8_t* qs, float* dx, int* bad, hipStream_t stream);
+
+// Per-block int32 sums of x's Q8 quants against W's blocks: out [N, K/32].
+hipError_t block_sums(int block_bytes, int N, int K, const int8_t* qs, const uint8_t* W, int32_t* out,
+                      hipStream_t stream);
+
+// W float [rows, K] -> GGUF blocks (block_bytes 18 or 34) bit-exact with ggml's reference
+// quantizers; *bad = 1 if W holds a NaN/Inf or a block scale overflows float16.
+hipError_t quantize_weights(int block_bytes, long long rows, int K, const float* W, uint8_t* out, int* bad,
+                            hipStream_t stream);
+
+// C = beta*C + alpha * A * B^T with A [M, lda] and B [N, ldb] of element type elem (0 fp32,
+// 1 fp16, 2 bf16), FP32 accumulation.  M <= 8 takes the row-streaming GEMV kernel.
+hipError_t gemm_tb(int elem, int M, int N, int K, float alpha, const void* A, int lda, const void* B, int ldb,
+                   float beta, float* C, int ldc, hipStream_t stream);
+
+// C = beta*C + alpha * op(A) * op(B), FP32, any transposes (small operands; attention helper).
+hipError_t sgemm_generic(bool trans_a, bool trans_b, int M, int N, int K, float alpha, const float* A, int lda,
+                         const float* B, int ldb, float beta, float* C, int ldc, hipStream_t stream);
+
+hipError_t silu(const float* in, float* out, long long n, hipStream_t stream);
+hipError_t softmax_rows(const float* in, float* out, int rows, int n, hipStream_t stream);
+hipError_t rms_norm(const float* x, const float* w, float* y, int rows, int n, double eps, hipStream_t stream);
+hipError_t rope(const float* x, const float* cos, const float* sin, float* y, int heads, int head_dim,
+                bool interleaved, hipStream_t stream);
+hipError_t fill(float* y, long long n, float value, hipStream_t stream);
+
+// Streams `bytes` of src (16-byte aligned) and writes one float per workgroup: the HBM read roof.
+hipError_t read_roof(const void* src, size_t bytes, float* sink, hipStream_t stream);
+
+}  // namespace smk

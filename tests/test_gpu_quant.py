@@ -1,0 +1,276 @@
+"""GPU parity of the quantized decode path against the CPU oracle (oracle/), through the C ABI.
+
+Bars (the reference's own, q4_0.hpp:25-30, q8_0.hpp:103-109):
+  * x's Q8 quants and FP32 scales: bit-exact;
+  * every per-block int32 sum: bit-exact;
+  * weight quantizers: byte-exact (llama.cpp fixture, special blocks, random);
+  * y: |y - y64| <= 2*(K/32 + 4)*2^-24 * sum_b |dw dx| sum_i |qw qx| against the float64
+    exact sum of the same quantized operands; non-finite x -> all NaN; K = 0 -> zeros.
+At the BASELINE shapes (8192x2048, 2048x8192, 14336x4096, 128256x4096) the same bound is
+checked in full, plus a checksum-of-checksums property on the rotated copies of the bench.
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from tests import gpu_util as g
+
+pytestmark = pytest.mark.gpu
+
+BB = {"q4_0": 18, "q8_0": 34}
+QUANT = {"q4_0": o.quantize_q4_0, "q8_0": o.quantize_q8_0}
+SHAPES = [(1, 32), (7, 64), (8, 96), (9, 128), (13, 160), (17, 352), (100, 4096), (33, 11008), (64, 2048),
+          (300, 2048), (1, 14336), (5, 8192)]
+
+
+def _inputs(fmt, N, K, seed, xscale=4.0):
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal((N, K)).astype(np.float32)
+    x = (rng.standard_normal(K) * xscale).astype(np.float32)
+    return x, QUANT[fmt](w)
+
+
+def d_gemv(fmt, x, wq, N, K, offset=0):
+    """y from smk_d_gemv_<fmt> on device copies; Wq placed `offset` bytes into its buffer."""
+    xd = g.dev(x)
+    staged = np.full(wq.nbytes + offset + 16, 0xEE, np.uint8)
+    staged[offset:offset + wq.nbytes] = wq.reshape(-1)
+    wbuf = g.dev(staged)
+    yd = g.empty(4 * N + 64)
+    g.call(f"smk_d_gemv_{fmt}", N, K, g.ptr(xd), g.ptr(wbuf, offset), g.ptr(yd), g.stream())
+    out = g.host(yd, np.float32)
+    assert (out[N:N + 16].view(np.uint32) == 0xEEEEEEEE).all(), "wrote past y[N)"
+    return out[:N]
+
+
+class TestXQuant:
+    @pytest.mark.parametrize("K", [32, 96, 2048, 4096, 14336])
+    def test_bit_exact(self, K):
+        x = (np.random.default_rng(K).standard_normal(K) * 3).astype(np.float32)
+        x[:32] = np.arange(-16, 16) + 0.5          # exact ties at d = 1? (amax 15.5): round half away
+        if K >= 96:
+            x[32:64] = 0.0                          # zero block
+            x[64:96] = np.float32(1e-39) * np.sign(np.random.default_rng(1).standard_normal(32)).astype(np.float32)
+        qs_ref, dx_ref = o.quantize_x_q8(x)
+        xd, qd, dd, bad = g.dev(x), g.empty(K), g.empty(4 * (K // 32)), g.empty(4, 0)
+        g.call("smk_d_quantize_x_q8", K, g.ptr(xd), g.ptr(qd), g.ptr(dd), g.ptr(bad), g.stream())
+        np.testing.assert_array_equal(g.host(qd, np.int8, K), qs_ref)
+        np.testing.assert_array_equal(g.host(dd, np.uint32, K // 32), dx_ref.view(np.uint32))
+        assert g.host(bad, np.int32)[0] == 0
+
+    def test_nonfinite_flag(self):
+        x = np.ones(256, np.float32)
+        x[77] = np.inf
+        xd, qd, dd, bad = g.dev(x), g.empty(256), g.empty(32), g.empty(4, 0)
+        g.call("smk_d_quantize_x_q8", 256, g.ptr(xd), g.ptr(qd), g.ptr(dd), g.ptr(bad), g.stream())
+        assert g.host(bad, np.int32)[0] == 1
+
+
+class TestBlockSums:
+    @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+    @pytest.mark.parametrize("N,K", [(7, 64), (33, 4096), (17, 352)])
+    def test_bit_exact(self, fmt, N, K):
+        x, wq = _inputs(fmt, N, K, N + K)
+        qs, _ = o.quantize_x_q8(x)
+        want = o.block_sums(fmt, qs, wq, N, K)
+        qd, wd, out = g.dev(qs), g.dev(wq), g.empty(4 * N * (K // 32))
+        g.call("smk_d_block_sums", BB[fmt], N, K, g.ptr(qd), g.ptr(wd), g.ptr(out), g.stream())
+        np.testing.assert_array_equal(g.host(out, np.int32, N * (K // 32)).reshape(N, -1), want)
+
+
+class TestQuantizeWeights:
+    def _run(self, fmt, w):
+        w = np.ascontiguousarray(w, np.float32)
+        rows, K = w.reshape(-1, w.shape[-1]).shape
+        out_bytes = rows * (K // 32) * BB[fmt]
+        wd, od, bad = g.dev(w), g.empty(out_bytes), g.empty(4, 0)
+        g.call("smk_d_quantize", BB[fmt], rows, K, g.ptr(wd), g.ptr(od), g.ptr(bad), g.stream())
+        return g.host(od, np.uint8, out_bytes), g.host(bad, np.int32)[0]
+
+    def test_q4_0_llama_cpp_fixture(self):
+        fx = np.load(os.path.join(os.path.dirname(__file__), "golden", "q4_0_ggml_v0.7.0.npz"), allow_pickle=False)
+        got, bad = self._run("q4_0", fx["w"])
+        assert bad == 0
+        np.testing.assert_array_equal(got.reshape(fx["blocks"].shape), fx["blocks"])
+
+    @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+    def test_random_and_special(self, fmt):
+        from tests.test_oracle import q8_special_rows
+        rng = np.random.default_rng(9)
+        special = q8_special_rows()[:, :128].repeat(2, axis=1)
+        if fmt == "q4_0":
+            special = special[[0, 1, 3, 4, 5]]  # row 2's scales overflow Q4_0's float16 scale
+        w = np.concatenate([rng.standard_normal((64, 256)).astype(np.float32) * 3, special])
+        w[0, :32] = np.where(np.arange(32) % 2, 1e-44, -1e-44).astype(np.float32)
+        w[1, :32] = 1.0
+        w[2, :32] = -0.0
+        got, bad = self._run(fmt, w)
+        assert bad == 0
+        np.testing.assert_array_equal(got.reshape(w.shape[0], -1), QUANT[fmt](w))
+
+    @pytest.mark.parametrize("fmt,limit", [("q4_0", 8 * 65520.0), ("q8_0", 127 * 65520.0)])
+    def test_rejections(self, fmt, limit):
+        for bad_v in (np.nan, np.inf, limit):
+            w = np.ones((3, 64), np.float32)
+            w[1, 40] = bad_v
+            assert self._run(fmt, w)[1] == 1
+        w = np.ones((3, 64), np.float32)
+        w[1, 40] = limit * 65504.0 / 65520.0
+        assert self._run(fmt, w)[1] == 0
+
+
+class TestGemv:
+    @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+    @pytest.mark.parametrize("N,K", SHAPES)
+    def test_within_bound(self, fmt, N, K):
+        x, wq = _inputs(fmt, N, K, N * 37 + K)
+        y = d_gemv(fmt, x, wq, N, K)
+        ref, mag = o.gemv_exact(fmt, x, wq, N, K)
+        err = np.abs(y.astype(np.float64) - ref)
+        assert (err <= o.gemv_bound(K, mag)).all(), f"max err/bound {np.max(err / o.gemv_bound(K, mag)):.3g}"
+
+    @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+    def test_extreme_quants(self, fmt):
+        N, K = 9, 4096
+        rng = np.random.default_rng(3)
+        w = np.where(rng.random((N, K)) < 0.5, -1.0, 1.0).astype(np.float32) * 1000.0
+        x = np.where(rng.random(K) < 0.5, -1.0, 1.0).astype(np.float32) * 1e3
+        wq = QUANT[fmt](w)
+        y = d_gemv(fmt, x, wq, N, K)
+        ref, mag = o.gemv_exact(fmt, x, wq, N, K)
+        assert (np.abs(y - ref) <= o.gemv_bound(K, mag)).all()
+
+    @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+    def test_nan_k0_n0(self, fmt):
+        w = np.full((9, 64), 0.25, np.float32)
+        for bad in (np.nan, np.inf, -np.inf):
+            x = np.ones(64, np.float32)
+            x[37] = bad
+            assert np.isnan(d_gemv(fmt, x, QUANT[fmt](w), 9, 64)).all()
+        assert (d_gemv(fmt, np.ones(0, np.float32), np.zeros(0, np.uint8), 5, 0) == 0).all()
+        yd = g.empty(64)
+        g.call(f"smk_d_gemv_{fmt}", 0, 32, 0, 0, g.ptr(yd), g.stream())
+        assert (g.host(yd, np.uint8) == 0xEE).all()
+
+    @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+    def test_two_byte_offset_takes_generic_path(self, fmt):
+        N, K = 13, 2048
+        x, wq = _inputs(fmt, N, K, 4)
+        a = d_gemv(fmt, x, wq, N, K)
+        b = d_gemv(fmt, x, wq, N, K, offset=2)
+        ref, mag = o.gemv_exact(fmt, x, wq, N, K)
+        assert (np.abs(b - ref) <= o.gemv_bound(K, mag)).all()
+        assert (np.abs(a - ref) <= o.gemv_bound(K, mag)).all()
+
+    @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+    @pytest.mark.parametrize("lpr", [8, 16, 32, 64])
+    def test_every_lane_split(self, fmt, lpr):
+        N, K = 77, 4096
+        x, wq = _inputs(fmt, N, K, lpr)
+        g.call("smk_set_gemv_tuning", lpr, 0)
+        try:
+            y = d_gemv(fmt, x, wq, N, K)
+        finally:
+            g.call("smk_set_gemv_tuning", 0, 0)
+        ref, mag = o.gemv_exact(fmt, x, wq, N, K)
+        assert (np.abs(y - ref) <= o.gemv_bound(K, mag)).all()
+
+
+class TestBatched:
+    @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+    @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+    def test_rows_equal_gemv_bitwise(self, fmt, M):
+        N, K = 96, 4096
+        rng = np.random.default_rng(M)
+        X = rng.standard_normal((M, K)).astype(np.float32)
+        X[M - 1, 5] = np.nan if M > 1 else X[M - 1, 5]   # one non-finite row: only that row is NaN
+        wq = QUANT[fmt](rng.standard_normal((N, K)).astype(np.float32))
+        xd, wd, yd = g.dev(X), g.dev(wq), g.empty(4 * M * N)
+        g.call(f"smk_d_gemm_{fmt}", M, N, K, g.ptr(xd), K, g.ptr(wd), g.ptr(yd), N, g.stream())
+        Y = g.host(yd, np.float32, M * N).reshape(M, N)
+        for m in range(M):
+            y1 = d_gemv(fmt, X[m], wq, N, K)
+            np.testing.assert_array_equal(Y[m].view(np.uint32), y1.view(np.uint32))
+
+
+class TestBaselineShapes:
+    """Full BASELINE.json configurations, checked against the exact float64 sum."""
+
+    @pytest.mark.parametrize("fmt,N,K,seed", [("q4_0", 8192, 2048, 0), ("q8_0", 8192, 2048, 1),
+                                              ("q8_0", 2048, 8192, 1), ("q4_0", 14336, 4096, 3)])
+    def test_config_shapes(self, fmt, N, K, seed):
+        x, w = o.synthetic(seed, [(K,), (N, K)], [1.0, 0.02])
+        wq = QUANT[fmt](w)
+        y = d_gemv(fmt, x, wq, N, K)
+        ref, mag = o.gemv_exact(fmt, x, wq, N, K)
+        assert (np.abs(y - ref) <= o.gemv_bound(K, mag)).all()
+
+    def test_lm_head_rows_and_checksum(self):
+        """Q4_0 lm_head 128256x4096: rows compared in slices; the sum over all outputs equals the
+        float64 exact sum within the summed bound (a checksum of checksums)."""
+        N, K = 128256, 4096
+        x, w = o.synthetic(3, [(K,), (N, K)], [1.0, 0.02])
+        wq = QUANT["q4_0"](w)
+        del w
+        y = d_gemv("q4_0", x, wq, N, K)
+        assert np.isfinite(y).all()
+        tot_ref, tot_mag = 0.0, 0.0
+        for lo in range(0, N, 16384):
+            hi = min(N, lo + 16384)
+            ref, mag = o.gemv_exact("q4_0", x, wq[lo:hi], hi - lo, K)
+            assert (np.abs(y[lo:hi] - ref) <= o.gemv_bound(K, mag)).all()
+            tot_ref += ref.sum()
+            tot_mag += mag.sum()
+        assert abs(float(np.sum(y.astype(np.float64))) - tot_ref) <= 2 * (K // 32 + 4) * 2.0 ** -24 * tot_mag
+
+
+class TestModuleHostPath:
+    """The pybind11 module (host arrays) on the same cases: it must equal the device entry point."""
+
+    @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+    def test_module_equals_device_entry(self, fmt):
+        import simd_ml_kernels as sk
+        N, K = 300, 2048
+        rng = np.random.default_rng(11)
+        w = rng.standard_normal((N, K)).astype(np.float32)
+        x = rng.standard_normal(K).astype(np.float32)
+        wq = getattr(sk, f"quantize_{fmt}")(w)
+        np.testing.assert_array_equal(wq, QUANT[fmt](w))
+        y = getattr(sk, f"gemv_{fmt}")(x, wq, N, K)
+        np.testing.assert_array_equal(y.view(np.uint32), d_gemv(fmt, x, wq, N, K).view(np.uint32))
+        # unaligned host buffers, read-only (pinned) weights
+        buf = np.empty(wq.size + 1, np.uint8)
+        buf[1:] = wq.ravel()
+        xbuf = np.empty(K + 1, np.float32)
+        xbuf[1:] = x
+        np.testing.assert_array_equal(getattr(sk, f"gemv_{fmt}")(xbuf[1:], buf[1:], N, K), y)
+        ro = wq.copy()
+        ro.setflags(write=False)
+        for _ in range(2):
+            np.testing.assert_array_equal(getattr(sk, f"gemv_{fmt}")(x, ro, N, K), y)
+
+    @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+    def test_module_edge_cases(self, fmt):
+        import simd_ml_kernels as sk
+        gemv, q = getattr(sk, f"gemv_{fmt}"), getattr(sk, f"quantize_{fmt}")
+        assert (gemv(np.ones(0, np.float32), np.zeros(0, np.uint8), 5, 0) == 0).all()
+        assert gemv(np.ones(32, np.float32), np.zeros(0, np.uint8), 0, 32).shape == (0,)
+        x = np.ones(64, np.float32)
+        x[3] = np.nan
+        assert np.isnan(gemv(x, q(np.ones((4, 64), np.float32)), 4, 64)).all()
+        w = np.ones((2, 64), np.float32)
+        w[0, 0] = np.inf
+        with pytest.raises(sk.ArgumentError):
+            q(w)
+
+    def test_module_gemm_rows(self):
+        import simd_ml_kernels as sk
+        rng = np.random.default_rng(2)
+        X = rng.standard_normal((32, 4096)).astype(np.float32)
+        wq = sk.quantize_q4_0(rng.standard_normal((200, 4096)).astype(np.float32))
+        Y = sk.gemm_q4_0(X, wq, 200, 4096)
+        for m in (0, 7, 8, 31):
+            np.testing.assert_array_equal(Y[m], sk.gemv_q4_0(X[m], wq, 200, 4096))
