@@ -166,11 +166,11 @@ def lowp_case(dev: Dev, fmt: str, N: int, K: int, seed: int, steps: int, warmup:
             "GFLOPs": 2 * N * K / sec / 1e9}
 
 
-def read_roof(dev: Dev, nbytes: int = 2 << 30, reps: int = 20) -> float:
+def read_roof(dev: Dev, nbytes: int = 2 << 30, reps: int = 20, nontemporal: int = 0) -> float:
     """Bytes/s of the library's HBM read-stream kernel over a 2 GiB buffer."""
     src = dev.abi.Buffer.filled(nbytes, 1)
     sink = dev.empty(4 * 4096)
-    run = lambda: dev.abi.call("smk_d_read_roof", src.ptr, nbytes, sink.ptr, dev.sp)
+    run = lambda: dev.abi.call("smk_d_read_roof", src.ptr, nbytes, sink.ptr, nontemporal, dev.sp)
     for _ in range(3):
         run()
     dev.stream.synchronize()

@@ -109,8 +109,9 @@ int smk_d_quantize(int block_bytes, long long rows, int K, const float* W, uint8
 /* Parity helpers: x's Q8 quants/scales (bad as above) and per-block int32 sums [N, K/32]. */
 int smk_d_quantize_x_q8(int K, const float* x, int8_t* qs, float* dx, int* bad, void* stream);
 int smk_d_block_sums(int block_bytes, int N, int K, const int8_t* qs, const uint8_t* Wq, int32_t* out, void* stream);
-/* HBM read roof: streams nbytes from src (16-byte aligned); sink: >= 2048 floats, never read back. */
-int smk_d_read_roof(const void* src, size_t nbytes, float* sink, void* stream);
+/* HBM read roof: streams nbytes from src (16-byte aligned) with plain or non-temporal 16-byte
+ * loads; sink: >= 2048 floats, never read back. */
+int smk_d_read_roof(const void* src, size_t nbytes, float* sink, int nontemporal, void* stream);
 
 /* Device memory, copies, streams, events and graphs, for callers without their own runtime
  * objects (the tests and bench.py use these; no other framework is loaded with the library). */
@@ -136,9 +137,10 @@ int smk_graph_destroy(void* graph_exec);
 /* HIP runtime version in use and the one the library was built against (HIP_VERSION). */
 int smk_runtime_version(int* runtime, int* built);
 
-/* Diagnostics: force the quantized GEMV's lanes per row / rows per workgroup (0 = automatic),
+/* Diagnostics: force the quantized GEMV's lanes per row, rows per workgroup, threads per
+ * workgroup and per-step row unroll (0 = automatic; the last two apply to one row of x),
  * and report the kernel a call would use ("pairs" or "generic"). */
-int smk_set_gemv_tuning(int lanes_per_row, int rows_per_wg);
+int smk_set_gemv_tuning(int lanes_per_row, int rows_per_wg, int threads, int unroll);
 const char* smk_gemv_path(int K, const void* Wq);
 
 #ifdef __cplusplus

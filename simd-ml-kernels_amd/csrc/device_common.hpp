@@ -39,27 +39,69 @@ __device__ __forceinline__ int finite_bits(float v) {
     return (__float_as_uint(v) & 0x7f800000u) != 0x7f800000u ? 1 : 0;
 }
 
-// Sum over aligned groups of `width` lanes (width a power of two <= 64); every lane
-// of the group gets the group's sum.
-template <int width>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+// ─── cross-lane reductions ──────────────────────────────────────────────────
+// Within a row of 16 lanes the partner values come through DPP (no LDS round trip):
+// quad_perm [1,0,3,2] and [2,3,0,1] pair lanes inside a quad, row_half_mirror pairs the two
+// quads of an 8-lane group, row_mirror the two halves of a row.  After the quad steps every
+// lane of a quad holds the quad's value, so a mirror partner is as good as an xor partner.
+// Across rows: ds_swizzle (xor 16 inside 32 lanes) and ds_bpermute (xor 32).
+constexpr int kDppQuadXor1 = 0xB1;
+constexpr int kDppQuadXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int ctrl>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, ctrl, 0xf, 0xf, false);
+}
+template <int ctrl>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<ctrl>(__float_as_int(v)));
+}
+
+struct AddOp {
+    template <class T>
+    __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
+};
+struct MaxOp {
+    __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+template <int width, class Op>
+__device__ __forceinline__ float group_reduce_f(float v, Op op) {
+    static_assert(width == 1 || width == 2 || width == 4 || width == 8 || width == 16 || width == 32 || width == 64, "");
+    if constexpr (width >= 2) v = op(v, dpp_f<kDppQuadXor1>(v));
+    if constexpr (width >= 4) v = op(v, dpp_f<kDppQuadXor2>(v));
+    if constexpr (width >= 8) v = op(v, dpp_f<kDppHalfMirror>(v));
+    if constexpr (width >= 16) v = op(v, dpp_f<kDppRowMirror>(v));
+    if constexpr (width >= 32) v = op(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f)));
+    if constexpr (width >= 64) v = op(v, __shfl_xor(v, 32, kWave));
     return v;
 }
 
 template <int width>
 __device__ __forceinline__ int group_sum_int(int v) {
-#pragma unroll
-    for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    if constexpr (width >= 2) v += dpp_i<kDppQuadXor1>(v);
+    if constexpr (width >= 4) v += dpp_i<kDppQuadXor2>(v);
+    if constexpr (width >= 8) v += dpp_i<kDppHalfMirror>(v);
+    if constexpr (width >= 16) v += dpp_i<kDppRowMirror>(v);
+    if constexpr (width >= 32) v += __builtin_amdgcn_ds_swizzle(v, 0x401f);
+    if constexpr (width >= 64) v += __shfl_xor(v, 32, kWave);
     return v;
 }
 
+// Sum / max over aligned groups of `width` lanes; every lane of the group gets the result.
 template <int width>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int off = width / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-    return v;
+__device__ __forceinline__ float group_sum(float v) { return group_reduce_f<width>(v, AddOp{}); }
+template <int width>
+__device__ __forceinline__ float group_max(float v) { return group_reduce_f<width>(v, MaxOp{}); }
+
+// Workgroup barrier that orders LDS only: it waits for this wave's LDS operations
+// (lgkmcnt) but not for its outstanding global loads, which stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {

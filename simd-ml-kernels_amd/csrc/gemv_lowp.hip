@@ -30,11 +30,11 @@ template <int E>
 __device__ __forceinline__ void load8(const void* row, size_t k, float (&v)[8]) {
     if constexpr (E == 0) {
         const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(row) + k);
-        const f32x4 a = __builtin_nontemporal_load(p), b = __builtin_nontemporal_load(p + 1);
+        const f32x4 a = p[0], b = p[1];
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
         v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     } else {
-        const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(row) + k));
+        const u32x4 t = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(row) + k);
         const uint32_t w[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {

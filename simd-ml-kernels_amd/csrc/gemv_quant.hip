@@ -51,42 +51,89 @@ __device__ __forceinline__ int x_dword_index(int b, int k, int pairs) {
     return 4 * (q * pairs + p) + (k & 3);
 }
 
-// Rows m < M of x ([M, ldx] floats) into lds_q ([M][K/4] dwords), lds_bias ([M][nb], Q4_0:
-// -8 * sum of the block's quants) and lds_dx ([M][nb]); bad[m] = 1 if row m is not finite.
-// 8 consecutive threads hold one 32-value block, 4 values each.
+// One quad of x (4 values of a 32-value block; 8 consecutive threads hold the block) into
+// the LDS quants, bias (Q4_0: -8 * sum of the block's quants) and scale; bad[m] = 1 when the
+// block holds a NaN/Inf.  All 8 threads of the block must call it together (DPP reductions).
+template <bool kPlanes, bool kBias>
+__device__ __forceinline__ void quantize_quad(const float (&v)[4], int m, int kq, int K, uint32_t* lds_q,
+                                              int* lds_bias, float* lds_dx, int* bad, bool live = true) {
+    const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
+    const int b = kq >> 3, k = kq & 7;
+    const int fin = finite_bits(v[0]) & finite_bits(v[1]) & finite_bits(v[2]) & finite_bits(v[3]);
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = group_max<8>(amax);
+    const float d = amax / 127.0f;                 // IEEE division (correctly rounded)
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    if (!(id <= 3.40282347e38f)) id = 0.0f;        // 1/d overflows: q = 0 (q8_0_scalar.cpp:249-252)
+    int q[4] = {0, 0, 0, 0};
+    if (fin) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = round_half_away(v[i] * id);
+    }
+    const uint32_t packed = (static_cast<uint32_t>(q[0]) & 0xffu) | ((static_cast<uint32_t>(q[1]) & 0xffu) << 8) |
+                            ((static_cast<uint32_t>(q[2]) & 0xffu) << 16) | (static_cast<uint32_t>(q[3]) << 24);
+    const int s = kBias ? group_sum_int<8>(q[0] + q[1] + q[2] + q[3]) : 0;
+    if (live) {
+        lds_q[m * quads + x_dword_index<kPlanes>(b, k, pairs)] = packed;
+        if (kBias && k == 0) lds_bias[m * nb + b] = -8 * s;
+        if (k == 0) lds_dx[m * nb + b] = d;
+        if (!fin) bad[m] = 1;
+    }
+}
+
+// The first PQ quads a thread quantizes are loaded into registers before the kernel issues
+// its weight loads, so that waiting for x does not wait for W (global loads retire in
+// order); quads past PQ * NT (very long rows) are loaded and quantized afterwards.
+template <int NT, int PQ>
+struct XPreload {
+    float v[PQ][4];
+    // Unconditional loads (an index past the end reloads quad 0): the wait for x then has
+    // a known count of younger loads and does not wait for the weights issued after it.
+    __device__ __forceinline__ void load(const float* __restrict__ x, int ldx, int M, int K) {
+        const int quads = K >> 2, total = M * quads;
+#pragma unroll
+        for (int p = 0; p < PQ; ++p) {
+            int qd = static_cast<int>(threadIdx.x) + p * NT;
+            qd = qd < total ? qd : 0;
+            const int m = qd / quads, kq = qd - m * quads;
+            const float* src = x + static_cast<size_t>(m) * ldx + 4 * kq;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[p][i] = src[i];
+        }
+    }
+    template <bool kPlanes, bool kBias>
+    __device__ __forceinline__ void quantize(const float* __restrict__ x, int ldx, int M, int K, uint32_t* lds_q,
+                                             int* lds_bias, float* lds_dx, int* bad) {
+        const int quads = K >> 2, total = M * quads;
+        // Every preloaded quad is processed (a quad past the end recomputes quad 0 and stores
+        // nothing), so no x value is consumed under a branch the compiler could sink its load
+        // into, past the weight loads.
+#pragma unroll
+        for (int p = 0; p < PQ; ++p) {
+            const int qd = static_cast<int>(threadIdx.x) + p * NT;
+            const bool live = qd < total;
+            const int qe = live ? qd : 0, m = qe / quads;
+            quantize_quad<kPlanes, kBias>(v[p], m, qe - m * quads, K, lds_q, lds_bias, lds_dx, bad, live);
+        }
+        for (int qd = static_cast<int>(threadIdx.x) + PQ * NT; qd < total; qd += NT) {
+            const int m = qd / quads, kq = qd - m * quads;
+            const float* src = x + static_cast<size_t>(m) * ldx + 4 * kq;
+            const float t[4] = {src[0], src[1], src[2], src[3]};
+            quantize_quad<kPlanes, kBias>(t, m, kq, K, lds_q, lds_bias, lds_dx, bad);
+        }
+    }
+};
+
+// All quads of x in a strided loop (the generic and standalone kernels).
 template <bool kPlanes, bool kBias>
 __device__ void quantize_x_into_lds(const float* __restrict__ x, int ldx, int M, int K, uint32_t* lds_q,
                                     int* lds_bias, float* lds_dx, int* bad) {
-    const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
-    const int total = M * quads;
+    const int quads = K >> 2, total = M * quads;
     for (int qd = threadIdx.x; qd < total; qd += blockDim.x) {
-        const int m = qd / quads;
-        const int kq = qd - m * quads;
-        const int b = kq >> 3, k = kq & 7;
+        const int m = qd / quads, kq = qd - m * quads;
         const float* src = x + static_cast<size_t>(m) * ldx + 4 * kq;
-        const float v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
-        const bool fin = (finite_bits(v0) & finite_bits(v1) & finite_bits(v2) & finite_bits(v3)) != 0;
-        float amax = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
-        amax = group_max<8>(amax);
-        const float d = amax / 127.0f;                 // IEEE division (correctly rounded)
-        float id = d != 0.0f ? 1.0f / d : 0.0f;
-        if (!(id <= 3.40282347e38f)) id = 0.0f;        // 1/d overflows: q = 0 (q8_0_scalar.cpp:249-252)
-        int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
-        if (fin) {
-            q0 = round_half_away(v0 * id);
-            q1 = round_half_away(v1 * id);
-            q2 = round_half_away(v2 * id);
-            q3 = round_half_away(v3 * id);
-        }
-        const uint32_t packed = (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8) |
-                                ((static_cast<uint32_t>(q2) & 0xffu) << 16) | (static_cast<uint32_t>(q3) << 24);
-        lds_q[m * quads + x_dword_index<kPlanes>(b, k, pairs)] = packed;
-        if (kBias) {
-            const int s = group_sum_int<8>(q0 + q1 + q2 + q3);
-            if (k == 0) lds_bias[m * nb + b] = -8 * s;
-        }
-        if (k == 0) lds_dx[m * nb + b] = d;
-        if (!fin) bad[m] = 1;
+        const float t[4] = {src[0], src[1], src[2], src[3]};
+        quantize_quad<kPlanes, kBias>(t, m, kq, K, lds_q, lds_bias, lds_dx, bad);
     }
 }
 
@@ -105,18 +152,22 @@ struct PairTraits<kQ8_0Bytes> {
     static constexpr bool kBias = false;
 };
 
+// Plain (cached) loads: neighbouring lanes' pairs share 128-byte lines and each line is
+// touched by the two 16-byte loads and the 4-byte load of a pair, so the vector L1 must keep
+// it between them (a non-temporal hint made those touches go back to L2: 11.2 -> 8.0 us at
+// 14336 x 4096 without it).
 template <int D>
 __device__ __forceinline__ void load_pair(const uint8_t* src, uint32_t (&w)[D]) {
     const u32x4a4* v = reinterpret_cast<const u32x4a4*>(src);
 #pragma unroll
     for (int i = 0; i < D / 4; ++i) {
-        const u32x4a4 t = __builtin_nontemporal_load(v + i);
+        const u32x4a4 t = v[i];
         w[4 * i + 0] = t.x;
         w[4 * i + 1] = t.y;
         w[4 * i + 2] = t.z;
         w[4 * i + 3] = t.w;
     }
-    w[D - 1] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src) + (D - 1));
+    w[D - 1] = reinterpret_cast<const uint32_t*>(src)[D - 1];
 }
 
 // Integer sums of one pair: sA for block 2p, sB for block 2p+1.  xq[0..3]: the four planes.
@@ -178,15 +229,18 @@ __device__ __forceinline__ float scale_a(const uint32_t (&w)[D]) { return half_b
 template <int D>
 __device__ __forceinline__ float scale_b(const uint32_t (&w)[D]) { return half_bits_to_float(w[D / 2] >> 16); }
 
-// BB: block bytes; LPR: lanes per row; U: rows per lane group in one step; MT: max rows of x.
-template <int BB, int LPR, int U, int MT>
-__global__ __launch_bounds__(kThreads) void gemv_pairs_kernel(int M, int N, int K, const float* __restrict__ x,
-                                                              int ldx, const uint8_t* __restrict__ W,
-                                                              float* __restrict__ y, int ldy, int rows_per_wg) {
+// BB: block bytes; LPR: lanes per row; U: rows per lane group in one step; MT: max rows of x;
+// NT: threads per workgroup.
+template <int BB, int LPR, int U, int MT, int NT>
+__global__ __launch_bounds__(NT) void gemv_pairs_kernel(int M, int N, int K, const float* __restrict__ x, int ldx,
+                                                        const uint8_t* __restrict__ W, float* __restrict__ y, int ldy,
+                                                        int rows_per_wg) {
     using T = PairTraits<BB>;
     constexpr int D = T::kDwords;
-    constexpr int G = kWave / LPR;           // rows side by side in one wave
-    constexpr int kRowsPerIter = 4 * G * U;  // rows one workgroup step covers
+    constexpr int G = kWave / LPR;                 // rows side by side in one wave
+    constexpr int kWaves = NT / kWave;
+    constexpr int kRowsPerIter = kWaves * G * U;   // rows one workgroup step covers
+    constexpr int PQ = (MT * 1024 + NT - 1) / NT < 4 ? (MT * 1024 + NT - 1) / NT : 4;  // up to 4 quads preloaded
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ int bad[MT];
 
@@ -205,23 +259,34 @@ __global__ __launch_bounds__(kThreads) void gemv_pairs_kernel(int M, int N, int 
     const int steps = iters * chunks;
 
     if (threadIdx.x < MT) bad[threadIdx.x] = 0;
+    lds_barrier();  // nothing global is in flight yet
 
+    // Every lane loads on every step, from a clamped (valid) row and pair when its own is
+    // past the end: with no load under a lane-dependent branch the compiler's wait counts
+    // stay exact, so the next step's loads remain in flight while this step computes.
     auto load_step = [&](int s, uint32_t (&w)[U][D]) {
         const int it = s / chunks, c = s - it * chunks;
-        const int p = j + c * LPR;
+        const int p = min(j + c * LPR, pairs - 1);
         const int rb = row0 + it * kRowsPerIter + (wave * U) * G + g;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int r = rb + u * G;
-            if (r < row_end && p < pairs) load_pair<D>(W + r * row_bytes + static_cast<size_t>(p) * (2 * BB), w[u]);
+            const int r = min(rb + u * G, row_end - 1);
+            load_pair<D>(W + r * row_bytes + static_cast<size_t>(p) * (2 * BB), w[u]);
         }
     };
 
+    // x first, then the first weight step: the x-quant below waits only for x.
+    XPreload<NT, PQ> xp;
+    xp.load(x, ldx, M, K);
+    // Keep every x load ahead of the weight loads: a compiler-only fence (no instruction)
+    // for the IR passes and a scheduling barrier for the machine scheduler.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t wa[U][D], wb[U][D];
-    if (steps > 0) load_step(0, wa);
-    __syncthreads();  // bad[] cleared
-    quantize_x_into_lds<true, T::kBias>(x, ldx, M, K, lds_q, lds_bias, lds_dx, bad);
-    __syncthreads();
+    load_step(0, wa);  // steps >= 1: K/32 >= 2 and every workgroup owns at least one row
+    __builtin_amdgcn_sched_barrier(0);
+    xp.template quantize<true, T::kBias>(x, ldx, M, K, lds_q, lds_bias, lds_dx, bad);
+    lds_barrier();  // x quants visible; the weight loads stay in flight
 
     float acc[U][MT];
 #pragma unroll
@@ -230,7 +295,7 @@ __global__ __launch_bounds__(kThreads) void gemv_pairs_kernel(int M, int N, int 
         for (int m = 0; m < MT; ++m) acc[u][m] = 0.0f;
 
     auto body = [&](int s, uint32_t (&cur)[U][D], uint32_t (&nxt)[U][D]) {
-        if (s + 1 < steps) load_step(s + 1, nxt);
+        load_step(s + 1 < steps ? s + 1 : s, nxt);  // the last step reloads its own (cached) bytes
         const int it = s / chunks, c = s - it * chunks;
         const int p = j + c * LPR;
         if (p < pairs) {
@@ -291,9 +356,9 @@ __global__ __launch_bounds__(kThreads) void gemv_generic_kernel(int M, int N, in
     int* lds_bias = reinterpret_cast<int*>(lds + M * quads);
     float* lds_dx = reinterpret_cast<float*>(lds_bias + M * nb);
     if (threadIdx.x < MT) bad[threadIdx.x] = 0;
-    __syncthreads();
+    lds_barrier();
     quantize_x_into_lds<false, kQ4>(x, ldx, M, K, lds_q, lds_bias, lds_dx, bad);
-    __syncthreads();
+    lds_barrier();
 
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int row0 = blockIdx.x * rows_per_wg;
@@ -388,6 +453,9 @@ __global__ void block_sums_kernel(int N, int K, const int8_t* __restrict__ qs, c
 
 // ─── host side ───────────────────────────────────────────────────────────────
 
+// Compute units of the device in use (set by the runtime at initialisation).
+int g_cus = 256;
+
 bool pair_path_ok(int K, const uint8_t* W) {
     return ((K >> 5) % 2 == 0) && (reinterpret_cast<uintptr_t>(W) % 4 == 0);
 }
@@ -400,11 +468,11 @@ int choose_lpr(int pairs) {
     return l;
 }
 
-template <int BB, int LPR, int U, int MT>
+template <int BB, int LPR, int U, int MT, int NT>
 hipError_t launch_pairs(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
                         int rows_per_wg, hipStream_t stream) {
     constexpr int G = kWave / LPR;
-    constexpr int kRowsPerIter = 4 * G * U;
+    constexpr int kRowsPerIter = (NT / kWave) * G * U;
     if (rows_per_wg <= 0) {
         // About two workgroups per CU on a 256-CU MI355X, in whole workgroup steps.
         const int want = (N + 511) / 512;
@@ -413,22 +481,34 @@ hipError_t launch_pairs(int M, int N, int K, const float* x, int ldx, const uint
     const int nb = K >> 5;
     const size_t lds = static_cast<size_t>(M) * (K + 8 * nb);
     const int grid = (N + rows_per_wg - 1) / rows_per_wg;
-    if (const hipError_t e = allow_lds(gemv_pairs_kernel<BB, LPR, U, MT>, lds); e != hipSuccess) return e;
-    hipLaunchKernelGGL((gemv_pairs_kernel<BB, LPR, U, MT>), dim3(grid), dim3(kThreads), lds, stream, M, N, K, x, ldx,
-                       W, y, ldy, rows_per_wg);
+    if (const hipError_t e = allow_lds(gemv_pairs_kernel<BB, LPR, U, MT, NT>, lds); e != hipSuccess) return e;
+    hipLaunchKernelGGL((gemv_pairs_kernel<BB, LPR, U, MT, NT>), dim3(grid), dim3(NT), lds, stream, M, N, K, x, ldx, W,
+                       y, ldy, rows_per_wg);
     return hipGetLastError();
 }
 
-template <int BB, int MT>
+template <int BB, int U, int MT, int NT>
 hipError_t launch_pairs_lpr(int lpr, int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y,
                             int ldy, int rows_per_wg, hipStream_t stream) {
-    constexpr int U = BB == kQ4_0Bytes ? (MT <= 2 ? 4 : 2) : (MT <= 2 ? 2 : 1);
     switch (lpr) {
-        case 64: return launch_pairs<BB, 64, U, MT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
-        case 32: return launch_pairs<BB, 32, U, MT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
-        case 16: return launch_pairs<BB, 16, U, MT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
-        default: return launch_pairs<BB, 8, U, MT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
+        case 64: return launch_pairs<BB, 64, U, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
+        case 32: return launch_pairs<BB, 32, U, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
+        case 16: return launch_pairs<BB, 16, U, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
+        default: return launch_pairs<BB, 8, U, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
     }
+}
+
+// One row of x: workgroup size and unroll are tunable.
+template <int BB>
+hipError_t launch_pairs_m1(int lpr, int nt, int u, int N, int K, const float* x, int ldx, const uint8_t* W, float* y,
+                           int ldy, int rpw, hipStream_t s) {
+#define SMK_PAIRS_M1(NT_, U_) \
+    if (nt == NT_ && u == U_) return launch_pairs_lpr<BB, U_, 1, NT_>(lpr, 1, N, K, x, ldx, W, y, ldy, rpw, s);
+    SMK_PAIRS_M1(256, 1) SMK_PAIRS_M1(256, 2) SMK_PAIRS_M1(256, 4)
+    SMK_PAIRS_M1(512, 1) SMK_PAIRS_M1(512, 2) SMK_PAIRS_M1(512, 4)
+    SMK_PAIRS_M1(1024, 1) SMK_PAIRS_M1(1024, 2) SMK_PAIRS_M1(1024, 4)
+#undef SMK_PAIRS_M1
+    return hipErrorInvalidValue;
 }
 
 template <int BB, int MT>
@@ -456,13 +536,33 @@ hipError_t gemv_quant_fmt(int M, int N, int K, const float* x, int ldx, const ui
             default: return launch_generic<BB, 8>(M, N, K, x, ldx, W, y, ldy, stream);
         }
     }
-    const int lpr = (t && t->lanes_per_row) ? t->lanes_per_row : choose_lpr((K >> 5) / 2);
-    const int rpw = t ? t->rows_per_wg : 0;
+    // The lane split fixes the summation order, so it depends on K only: every row of a
+    // batched call then equals the single-row call bit for bit.  64 lanes per row once a row
+    // holds >= 128 pairs, else 32 (measured best on MI355X for the BASELINE shapes).
+    const int pairs = (K >> 5) / 2;
+    const int lpr = (t && t->lanes_per_row) ? t->lanes_per_row
+                                            : (pairs >= 128 ? 64 : (pairs >= 32 ? 32 : choose_lpr(pairs)));
+    int rpw = t ? t->rows_per_wg : 0;
+    if (mt == 1) {
+        // One row of x (decode).  Measured on MI355X over the BASELINE shapes (9.4 MB to 295 MB
+        // of weights): one pair per lane per step; 1024-thread workgroups for small and very
+        // large matrices, 512 in between; 1, 2 or 4 workgroups per CU with the rows split evenly.
+        const double bytes = static_cast<double>(N) * (K >> 5) * BB;
+        const int nt_auto = (bytes < 24e6 || bytes >= 128e6) ? 1024 : 512;
+        const int per_cu = bytes < 24e6 ? 1 : (bytes < 128e6 ? 2 : 4);
+        if (rpw <= 0) rpw = std::max(1, (N + g_cus * per_cu - 1) / (g_cus * per_cu));
+        // No more waves than rows: a wave covers 64 / lpr rows per step.
+        int nt = (t && t->threads) ? t->threads : nt_auto;
+        if (!(t && t->threads))
+            while (nt > 256 && nt > rpw * lpr) nt /= 2;
+        const int u = (t && t->unroll) ? t->unroll : 1;
+        return launch_pairs_m1<BB>(lpr, nt, u, N, K, x, ldx, W, y, ldy, rpw, stream);
+    }
+    constexpr int U2 = BB == kQ4_0Bytes ? 4 : 2, U4 = BB == kQ4_0Bytes ? 2 : 1;
     switch (mt) {
-        case 1: return launch_pairs_lpr<BB, 1>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
-        case 2: return launch_pairs_lpr<BB, 2>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
-        case 4: return launch_pairs_lpr<BB, 4>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
-        default: return launch_pairs_lpr<BB, 8>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
+        case 2: return launch_pairs_lpr<BB, U2, 2, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
+        case 4: return launch_pairs_lpr<BB, U4, 4, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
+        default: return launch_pairs_lpr<BB, U4, 8, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
     }
 }
 
@@ -505,6 +605,8 @@ hipError_t gemv_quant(int block_bytes, int M, int N, int K, const float* x, int 
 }
 
 const char* gemv_quant_path(int, int, int K, const uint8_t* W) { return pair_path_ok(K, W) ? "pairs" : "generic"; }
+
+void set_compute_units(int cus) { g_cus = cus > 0 ? cus : 256; }
 
 hipError_t quantize_x_q8(int K, const float* x, int8_t* qs, float* dx, int* bad, hipStream_t stream) {
     if (K <= 0) return hipSuccess;

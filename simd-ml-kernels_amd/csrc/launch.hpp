@@ -16,6 +16,8 @@ constexpr int kQ8_0Bytes = 34;
 struct GemvTuning {
     int lanes_per_row = 0;  // 8, 16, 32 or 64 lanes share one row of W
     int rows_per_wg = 0;    // rows of W per workgroup
+    int threads = 0;        // threads per workgroup: 256, 512 or 1024 (one row of x only)
+    int unroll = 0;         // rows per lane group per step: 1, 2 or 4 (one row of x only)
 };
 
 // y[m*ldy + n] = sum_k x[m*ldx + k] * W[n][k] for m < M (M <= 8), W in GGUF Q4_0 (block_bytes 18)
@@ -23,6 +25,9 @@ struct GemvTuning {
 // with a NaN or +-Inf makes its whole row of y NaN; K == 0 gives zeros.  K % 32 == 0.
 hipError_t gemv_quant(int block_bytes, int M, int N, int K, const float* x, int ldx, const uint8_t* W,
                       float* y, int ldy, hipStream_t stream, const GemvTuning* tuning = nullptr);
+
+// Compute units of the device (workgroup counts of the GEMV follow it).
+void set_compute_units(int cus);
 
 // The kernel gemv_quant would launch, for reports: "pairs" or "generic".
 const char* gemv_quant_path(int block_bytes, int N, int K, const uint8_t* W);
@@ -56,7 +61,8 @@ hipError_t rope(const float* x, const float* cos, const float* sin, float* y, in
                 bool interleaved, hipStream_t stream);
 hipError_t fill(float* y, long long n, float value, hipStream_t stream);
 
-// Streams `bytes` of src (16-byte aligned) and writes one float per workgroup: the HBM read roof.
-hipError_t read_roof(const void* src, size_t bytes, float* sink, hipStream_t stream);
+// Streams `bytes` of src (16-byte aligned) with plain or non-temporal 16-byte loads and writes
+// nothing (unless an improbable xor matches): the HBM read roof.
+hipError_t read_roof(const void* src, size_t bytes, float* sink, bool nontemporal, hipStream_t stream);
 
 }  // namespace smk

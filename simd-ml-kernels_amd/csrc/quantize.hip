@@ -122,18 +122,25 @@ __global__ __launch_bounds__(256) void quantize_weights_kernel(long long blocks,
 }
 
 // Each thread sums 16-byte words with a stride of the whole grid: a pure HBM read stream.
+template <bool kNT>
+__device__ __forceinline__ u32x4 ld16(const u32x4* p) {
+    if constexpr (kNT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+
+template <bool kNT>
 __global__ __launch_bounds__(256) void read_roof_kernel(const u32x4* __restrict__ src, size_t n16,
                                                         float* __restrict__ sink) {
     uint32_t acc = 0;
     const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
     size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
     for (; i + 3 * stride < n16; i += 4 * stride) {
-        const u32x4 a = __builtin_nontemporal_load(src + i), b = __builtin_nontemporal_load(src + i + stride);
-        const u32x4 c = __builtin_nontemporal_load(src + i + 2 * stride), d = __builtin_nontemporal_load(src + i + 3 * stride);
+        const u32x4 a = ld16<kNT>(src + i), b = ld16<kNT>(src + i + stride);
+        const u32x4 c = ld16<kNT>(src + i + 2 * stride), d = ld16<kNT>(src + i + 3 * stride);
         acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
     }
     for (; i < n16; i += stride) {
-        const u32x4 a = __builtin_nontemporal_load(src + i);
+        const u32x4 a = ld16<kNT>(src + i);
         acc ^= a.x ^ a.y ^ a.z ^ a.w;
     }
     if (acc == 0x9e3779b9u) sink[blockIdx.x] = 1.0f;  // keeps the loads; practically never taken
@@ -157,11 +164,14 @@ hipError_t quantize_weights(int block_bytes, long long rows, int K, const float*
     return hipGetLastError();
 }
 
-hipError_t read_roof(const void* src, size_t bytes, float* sink, hipStream_t s) {
+hipError_t read_roof(const void* src, size_t bytes, float* sink, bool nontemporal, hipStream_t s) {
     const size_t n16 = bytes / 16;
     if (n16 == 0) return hipSuccess;
     const int grid = 256 * 8;
-    hipLaunchKernelGGL(read_roof_kernel, dim3(grid), dim3(256), 0, s, static_cast<const u32x4*>(src), n16, sink);
+    if (nontemporal)
+        hipLaunchKernelGGL(read_roof_kernel<true>, dim3(grid), dim3(256), 0, s, static_cast<const u32x4*>(src), n16, sink);
+    else
+        hipLaunchKernelGGL(read_roof_kernel<false>, dim3(grid), dim3(256), 0, s, static_cast<const u32x4*>(src), n16, sink);
     return hipGetLastError();
 }
 

@@ -87,6 +87,7 @@ Device& device() {
         }
         r.id = want;
         r.status = SMK_OK;
+        smk::set_compute_units(r.prop.multiProcessorCount);
         return r;
     }();
     return d;
@@ -569,10 +570,10 @@ int smk_d_block_sums(int bb, int N, int K, const int8_t* qs, const uint8_t* Wq, 
     return ok();
 }
 
-int smk_d_read_roof(const void* src, size_t nbytes, float* sink, void* stream) {
+int smk_d_read_roof(const void* src, size_t nbytes, float* sink, int nontemporal, void* stream) {
     if (reinterpret_cast<uintptr_t>(src) % 16) return fail(SMK_ERR_ARGUMENT, "src must be 16-byte aligned");
     if (const int rc = use_device()) return rc;
-    SMK_HIP(smk::read_roof(src, nbytes, sink, S(stream)), "read_roof launch");
+    SMK_HIP(smk::read_roof(src, nbytes, sink, nontemporal != 0, S(stream)), "read_roof launch");
     return ok();
 }
 
@@ -687,12 +688,17 @@ int smk_runtime_version(int* runtime, int* built) {
     return ok();
 }
 
-int smk_set_gemv_tuning(int lanes_per_row, int rows_per_wg) {
+int smk_set_gemv_tuning(int lanes_per_row, int rows_per_wg, int threads, int unroll) {
     if (lanes_per_row != 0 && lanes_per_row != 8 && lanes_per_row != 16 && lanes_per_row != 32 && lanes_per_row != 64)
         return fail(SMK_ERR_ARGUMENT, "lanes_per_row must be 0, 8, 16, 32 or 64");
     if (rows_per_wg < 0) return fail(SMK_ERR_ARGUMENT, "rows_per_wg must be >= 0");
+    if (threads != 0 && threads != 256 && threads != 512 && threads != 1024)
+        return fail(SMK_ERR_ARGUMENT, "threads must be 0, 256, 512 or 1024");
+    if (unroll != 0 && unroll != 1 && unroll != 2 && unroll != 4) return fail(SMK_ERR_ARGUMENT, "unroll must be 0, 1, 2 or 4");
     g_tuning.lanes_per_row = lanes_per_row;
     g_tuning.rows_per_wg = rows_per_wg;
+    g_tuning.threads = threads;
+    g_tuning.unroll = unroll;
     return ok();
 }
 

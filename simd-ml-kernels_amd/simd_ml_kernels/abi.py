@@ -58,7 +58,7 @@ SIGNATURES = {
     "smk_d_quantize": [_i, _ll, _i, _p, _p, _p, _p],
     "smk_d_quantize_x_q8": [_i, _p, _p, _p, _p, _p],
     "smk_d_block_sums": [_i, _i, _i, _p, _p, _p, _p],
-    "smk_d_read_roof": [_p, _sz, _p, _p],
+    "smk_d_read_roof": [_p, _sz, _p, _i, _p],
     "smk_malloc": [ctypes.POINTER(_p), _sz],
     "smk_free": [_p],
     "smk_memcpy_h2d": [_p, _p, _sz],
@@ -78,7 +78,7 @@ SIGNATURES = {
     "smk_graph_launch": [_p, _p],
     "smk_graph_destroy": [_p],
     "smk_runtime_version": [ctypes.POINTER(_i), ctypes.POINTER(_i)],
-    "smk_set_gemv_tuning": [_i, _i],
+    "smk_set_gemv_tuning": [_i, _i, _i, _i],
     "smk_gemv_path": [_i, _p],
 }
 _RESTYPE = {"smk_last_error": ctypes.c_char_p, "smk_version": ctypes.c_char_p, "smk_gemv_path": ctypes.c_char_p}

@@ -170,11 +170,11 @@ class TestGemv:
     def test_every_lane_split(self, fmt, lpr):
         N, K = 77, 4096
         x, wq = _inputs(fmt, N, K, lpr)
-        g.call("smk_set_gemv_tuning", lpr, 0)
+        g.call("smk_set_gemv_tuning", lpr, 0, 0, 0)
         try:
             y = d_gemv(fmt, x, wq, N, K)
         finally:
-            g.call("smk_set_gemv_tuning", 0, 0)
+            g.call("smk_set_gemv_tuning", 0, 0, 0, 0)
         ref, mag = o.gemv_exact(fmt, x, wq, N, K)
         assert (np.abs(y - ref) <= o.gemv_bound(K, mag)).all()
 
