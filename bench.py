@@ -179,6 +179,35 @@ def read_roof(dev: Dev, nbytes: int = 2 << 30, reps: int = 20, nontemporal: int 
     return nbytes * reps / sec
 
 
+def copy_roof(dev: Dev, nbytes: int = 256 << 20, reps: int = 5) -> float:
+    """Bytes/s (read + write) of the library's plain copy kernel over 256 MiB.  Under a PMC run its
+    FETCH_SIZE and WRITE_SIZE per dispatch calibrate the counters: it moves exactly nbytes each way."""
+    src = dev.abi.Buffer.filled(nbytes, 3)
+    dst = dev.empty(nbytes)
+    run = lambda: dev.abi.call("smk_d_copy", dst.ptr, src.ptr, nbytes, dev.sp)
+    run()
+    dev.stream.synchronize()
+    sec = dev.timed(run, reps)
+    del src, dst
+    return 2 * nbytes * reps / sec
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4_0_8192x2048_hbm_traffic.md")
+
+
+def profiled_traffic() -> int | None:
+    """HBM bytes per launch of the headline kernel, from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by the copy/read-roof calibration)."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(N: int, K: int, budget_s: float) -> dict | None:
     """The reference's own gemv_q4_0 (widest table this CPU runs, OpenMP on every allowed core)
     on a bounded sample of the headline workload, weights rotated past the host caches."""
@@ -247,6 +276,7 @@ def main() -> int:
         for M in (2, 4, 8):
             cases[f"q4_0_M{M}_14336x4096"] = quant_case(dev, "q4_0", 14336, 4096, 4, st, wu, args.mode, M=M)
     roof = read_roof(dev)
+    copy = copy_roof(dev)
     sec = head["us"] * 1e-6
     achieved = head["weight_bytes"] / sec
     out = {
@@ -266,10 +296,13 @@ def main() -> int:
                                f"{math.ceil(ROTATE_BYTES / head['weight_bytes']) + 1} rotated weight copies, "
                                f"launch mode {args.mode}"},
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM, 4), "traffic": None},
+                     "frac": round(achieved / PEAK_HBM, 4), "traffic": profiled_traffic(),
+                     "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0)",
+                     "algorithmic_bytes": head["weight_bytes"]},
         "pct_hbm_peak": round(100 * achieved / PEAK_HBM, 2),
         "hbm_read_roof_GBps": round(roof / 1e9, 1),
         "pct_read_roof": round(100 * achieved / roof, 2),
+        "hbm_copy_GBps": round(copy / 1e9, 1),
         "GFLOPs": round(head["GFLOPs"], 1),
         "GBps_weights_x_y": round(head["GBps_weights_x_y"], 2),
         "cases": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}

@@ -112,6 +112,9 @@ int smk_d_block_sums(int block_bytes, int N, int K, const int8_t* qs, const uint
 /* HBM read roof: streams nbytes from src (16-byte aligned) with plain or non-temporal 16-byte
  * loads; sink: >= 2048 floats, never read back. */
 int smk_d_read_roof(const void* src, size_t nbytes, float* sink, int nontemporal, void* stream);
+/* Device-to-device copy of nbytes with a plain 16-byte vector kernel (async on stream); it reads
+ * and writes exactly nbytes, which also makes it the calibration kernel of the HBM byte counters. */
+int smk_d_copy(void* dst, const void* src, size_t nbytes, void* stream);
 
 /* Device memory, copies, streams, events and graphs, for callers without their own runtime
  * objects (the tests and bench.py use these; no other framework is loaded with the library). */

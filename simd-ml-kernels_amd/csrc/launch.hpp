@@ -64,5 +64,8 @@ hipError_t fill(float* y, long long n, float value, hipStream_t stream);
 // Streams `bytes` of src (16-byte aligned) with plain or non-temporal 16-byte loads and writes
 // nothing (unless an improbable xor matches): the HBM read roof.
 hipError_t read_roof(const void* src, size_t bytes, float* sink, bool nontemporal, hipStream_t stream);
+// Device-to-device copy with a plain vector kernel (hipMemcpyAsync when a pointer is not
+// 16-byte aligned).
+hipError_t copy_bytes(void* dst, const void* src, size_t bytes, hipStream_t stream);
 
 }  // namespace smk

@@ -146,7 +146,40 @@ __global__ __launch_bounds__(256) void read_roof_kernel(const u32x4* __restrict_
     if (acc == 0x9e3779b9u) sink[blockIdx.x] = 1.0f;  // keeps the loads; practically never taken
 }
 
+// Grid-stride copy of 16-byte words (both pointers 16-byte aligned); the last nbytes % 16
+// bytes are copied one by one by the first thread.  Reads and writes exactly nbytes each, so
+// it also calibrates the HBM byte counters.
+__global__ __launch_bounds__(256) void copy_kernel(u32x4* __restrict__ dst, const u32x4* __restrict__ src,
+                                                   size_t n16, const uint8_t* __restrict__ tail_src,
+                                                   uint8_t* __restrict__ tail_dst, int tail) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const u32x4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+        dst[i] = a;
+        dst[i + stride] = b;
+        dst[i + 2 * stride] = c;
+        dst[i + 3 * stride] = d;
+    }
+    for (; i < n16; i += stride) dst[i] = src[i];
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        for (int t = 0; t < tail; ++t) tail_dst[t] = tail_src[t];
+}
+
 }  // namespace
+
+hipError_t copy_bytes(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    if (bytes == 0) return hipSuccess;
+    if ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) % 16 != 0)
+        return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s);
+    const size_t n16 = bytes / 16;
+    const int grid = static_cast<int>(std::max<size_t>(1, std::min<size_t>((n16 + 1023) / 1024, 256 * 8)));
+    const auto* s8 = static_cast<const uint8_t*>(src) + n16 * 16;
+    auto* d8 = static_cast<uint8_t*>(dst) + n16 * 16;
+    hipLaunchKernelGGL(copy_kernel, dim3(grid), dim3(256), 0, s, static_cast<u32x4*>(dst),
+                       static_cast<const u32x4*>(src), n16, s8, d8, static_cast<int>(bytes % 16));
+    return hipGetLastError();
+}
 
 hipError_t quantize_weights(int block_bytes, long long rows, int K, const float* W, uint8_t* out, int* bad,
                             hipStream_t s) {

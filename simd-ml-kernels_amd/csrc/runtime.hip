@@ -577,6 +577,13 @@ int smk_d_read_roof(const void* src, size_t nbytes, float* sink, int nontemporal
     return ok();
 }
 
+int smk_d_copy(void* dst, const void* src, size_t nbytes, void* stream) {
+    if (nbytes && (!dst || !src)) return fail(SMK_ERR_ARGUMENT, "null pointer");
+    if (const int rc = use_device()) return rc;
+    SMK_HIP(smk::copy_bytes(dst, src, nbytes, S(stream)), "copy launch");
+    return ok();
+}
+
 int smk_malloc(void** p, size_t n) {
     if (const int rc = use_device()) return rc;
     SMK_HIP(hipMalloc(p, n), "hipMalloc");

@@ -59,6 +59,7 @@ SIGNATURES = {
     "smk_d_quantize_x_q8": [_i, _p, _p, _p, _p, _p],
     "smk_d_block_sums": [_i, _i, _i, _p, _p, _p, _p],
     "smk_d_read_roof": [_p, _sz, _p, _i, _p],
+    "smk_d_copy": [_p, _p, _sz, _p],
     "smk_malloc": [ctypes.POINTER(_p), _sz],
     "smk_free": [_p],
     "smk_memcpy_h2d": [_p, _p, _sz],
