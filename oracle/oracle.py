@@ -342,6 +342,50 @@ def rms_norm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
     return weight * (x * np.float32(1.0 / math.sqrt(float(var) + eps)))
 
 
+def numpy_sum_f32(a: np.ndarray, bufsize: int = 8192) -> np.float32:
+    """np.add.reduce of a contiguous float32 vector, restated: the reduction runs over chunks
+    of the ufunc buffer size (8192), each chunk summed pairwise and the chunk sums added in
+    order to -0.0.  The model the GPU RMSNorm follows; checked against np.add.reduce."""
+    a = np.ascontiguousarray(a, np.float32)
+    r = np.float32(-0.0)
+    for s in range(0, a.size, bufsize):
+        r = np.float32(r + pairwise_sum_f32(a[s:s + bufsize]))
+    return r
+
+
+def pairwise_sum_f32(a: np.ndarray) -> np.float32:
+    """numpy's float32 pairwise summation (numpy/_core/src/umath/loops_utils.h.src,
+    pairwise_sum): n < 8 sequential from 0; n <= 128 eight interleaved accumulators combined
+    ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) then the n % 8 tail in order; larger n split at
+    n2 = n/2 - (n/2) % 8."""
+    a = np.ascontiguousarray(a, np.float32)
+
+    def rec(lo: int, n: int) -> np.float32:
+        if n < 8:
+            r = np.float32(0)
+            for i in range(n):
+                r = np.float32(r + a[lo + i])
+            return r
+        if n <= 128:
+            r = [a[lo + k] for k in range(8)]
+            i = 8
+            while i < n - (n % 8):
+                for k in range(8):
+                    r[k] = np.float32(r[k] + a[lo + i + k])
+                i += 8
+            res = np.float32(np.float32(np.float32(r[0] + r[1]) + np.float32(r[2] + r[3])) +
+                             np.float32(np.float32(r[4] + r[5]) + np.float32(r[6] + r[7])))
+            while i < n:
+                res = np.float32(res + a[lo + i])
+                i += 1
+            return res
+        n2 = n // 2
+        n2 -= n2 % 8
+        return np.float32(rec(lo, n2) + rec(lo + n2, n - n2))
+
+    return rec(0, a.size)
+
+
 def rms_norm64(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
     x64 = np.asarray(x, np.float64)
     return np.asarray(weight, np.float64) * x64 / math.sqrt(float(np.mean(x64 * x64)) + eps)

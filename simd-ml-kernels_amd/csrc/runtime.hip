@@ -389,7 +389,7 @@ int smk_quantize_q8_0(const float* W, int N, int K, uint8_t* out) { return host_
 
 int smk_rms_norm(const float* x, const float* w, float* y, int rows, int n, double eps) {
     if (rows <= 0 || n <= 0) return ok();
-    if (n > 32768) return fail(SMK_ERR_ARGUMENT, "rms_norm: n must be <= 32768");
+    if (rows < 0 || n < 0) return fail(SMK_ERR_ARGUMENT, "rms_norm: rows and n must be >= 0");
     Ctx* c;
     if (const int rc = context(&c)) return rc;
     const size_t bytes = static_cast<size_t>(rows) * n * 4;
@@ -533,7 +533,7 @@ int smk_d_softmax(const float* in, float* out, int rows, int n, void* stream) {
 }
 
 int smk_d_rms_norm(const float* x, const float* w, float* y, int rows, int n, double eps, void* stream) {
-    if (n > 32768) return fail(SMK_ERR_ARGUMENT, "rms_norm: n must be <= 32768");
+    if (rows < 0 || n < 0) return fail(SMK_ERR_ARGUMENT, "rms_norm: rows and n must be >= 0");
     if (const int rc = use_device()) return rc;
     SMK_HIP(smk::rms_norm(x, w, y, rows, n, eps, S(stream)), "rms_norm launch");
     return ok();

@@ -9,6 +9,7 @@ the reference's own compiled kernels, bit for bit.  The last class plants
 plausible mistakes in copies of the oracle and shows the checks catch them.
 """
 
+import math
 import os
 
 import numpy as np
@@ -389,3 +390,92 @@ class TestPlantedMistakes:
         C = o.gemm_tb("fp32", A, W.T.copy())  # W^T passed where W is expected
         bound = o.gemm_bound(33, np.abs(A.astype(np.float64)) @ np.abs(W.astype(np.float64)).T)
         assert not (np.abs(C - A.astype(np.float64) @ W.astype(np.float64).T) <= bound).all()
+
+
+class TestLlamaFormulas:
+    """The numpy formulas of examples/llama/llama.py that the GPU kernels restate, pinned by
+    numpy itself (the reduction model) and by float64 mathematics (norm, rotation, frequencies)."""
+
+    @pytest.mark.parametrize("n", [1, 7, 8, 9, 100, 128, 129, 136, 260, 1000, 2048, 8191, 8192, 8193, 14336, 20000])
+    def test_numpy_sum_model_equals_add_reduce(self, n):
+        rng = np.random.default_rng(n)
+        for s in (-3, 0, 3):
+            q = (rng.standard_normal(n) * 10.0 ** s).astype(np.float32) ** 2
+            got = o.numpy_sum_f32(q)
+            assert got.view(np.uint32) == np.float32(np.add.reduce(q, dtype=np.float32)).view(np.uint32)
+
+    def test_unchunked_pairwise_differs_above_8192(self):
+        """A single pairwise tree over 14336 values is not numpy's sum (it reduces by 8192-chunks)."""
+        rng = np.random.default_rng(0)
+        differs = 0
+        for _ in range(20):
+            q = (rng.standard_normal(14336) * 30).astype(np.float32) ** 2
+            differs += o.pairwise_sum_f32(q).view(np.uint32) != np.float32(np.add.reduce(q)).view(np.uint32)
+        assert differs > 0
+
+    def test_rms_norm_close_to_float64(self):
+        rng = np.random.default_rng(1)
+        for n in (64, 2048, 14336):
+            x = rng.standard_normal(n).astype(np.float32) * np.float32(7)
+            w = rng.standard_normal(n).astype(np.float32)
+            y, y64 = o.rms_norm(x, w, 1e-5), o.rms_norm64(x, w, 1e-5)
+            # var: sum error <= log2(n) u, division/scale/products a few more roundings.
+            assert (np.abs(y - y64) <= (math.log2(n) + 8) * 2.0 ** -24 * np.abs(y64) + 1e-30).all()
+
+    def test_rms_norm_planted_float32_scale_fails(self):
+        """Computing 1/sqrt(var + eps) in float32 (instead of float64) changes some outputs."""
+        rng = np.random.default_rng(2)
+        changed = 0
+        for _ in range(50):
+            x = rng.standard_normal(2048).astype(np.float32)
+            w = np.ones(2048, np.float32)
+            var = np.mean(x * x, dtype=np.float32)
+            wrong = w * (x * (np.float32(1) / np.sqrt(var + np.float32(1e-5))))
+            changed += not np.array_equal(wrong, o.rms_norm(x, w, 1e-5))
+        assert changed > 0
+
+    @pytest.mark.parametrize("interleaved", [True, False])
+    def test_rope_is_a_rotation(self, interleaved):
+        rng = np.random.default_rng(3)
+        hd = 64
+        inv = o.rope_inv_freq(hd, 500000.0, None)
+        pos = 123
+        cos, sin = o.rope_cos_sin(inv, pos)
+        x = rng.standard_normal((8, hd)).astype(np.float32)
+        y = o.rope(x, cos, sin, interleaved).astype(np.float64)
+        ang = pos * inv.astype(np.float64)
+        if interleaved:
+            z = (x[:, 0::2] + 1j * x[:, 1::2]).astype(np.complex128) * np.exp(1j * ang)
+            ref = np.empty((8, hd))
+            ref[:, 0::2], ref[:, 1::2] = z.real, z.imag
+        else:
+            z = (x[:, :hd // 2] + 1j * x[:, hd // 2:]).astype(np.complex128) * np.exp(1j * ang)
+            ref = np.concatenate([z.real, z.imag], axis=1)
+        assert np.abs(y - ref).max() < 1e-4  # angles are float32 (pos * inv_freq rounded), as in the example
+        np.testing.assert_allclose(np.linalg.norm(y, axis=1), np.linalg.norm(x.astype(np.float64), axis=1), rtol=1e-6)
+
+    def test_rope_planted_swapped_sign_fails(self):
+        rng = np.random.default_rng(4)
+        cos, sin = o.rope_cos_sin(o.rope_inv_freq(64, 500000.0, None), 5)
+        x = rng.standard_normal((2, 64)).astype(np.float32)
+        good = o.rope(x, cos, sin, True)
+        a, b = x[:, 0::2], x[:, 1::2]
+        bad = np.empty_like(x)
+        bad[:, 0::2], bad[:, 1::2] = a * cos[:32] + b * sin[:32], b * cos[:32] - a * sin[:32]
+        assert not np.allclose(good, bad)
+
+    def test_rope_inv_freq_default_and_llama3(self):
+        hd, theta = 64, 500000.0
+        base = o.rope_inv_freq(hd, theta, None).astype(np.float64)
+        np.testing.assert_allclose(base, theta ** (-np.arange(0, hd, 2) / hd), rtol=2e-6)
+        rs = {"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+              "original_max_position_embeddings": 8192}
+        sc = o.rope_inv_freq(hd, theta, rs).astype(np.float64)
+        wl = 2 * math.pi / base
+        hi = wl < 8192 / 4.0
+        lo = wl > 8192 / 1.0
+        np.testing.assert_allclose(sc[hi], base[hi], rtol=1e-6)       # short wavelengths kept
+        np.testing.assert_allclose(sc[lo], base[lo] / 32.0, rtol=1e-6)  # long ones divided by factor
+        mid = ~hi & ~lo
+        s = (8192 / wl[mid] - 1.0) / 3.0
+        np.testing.assert_allclose(sc[mid], (1 - s) * base[mid] / 32.0 + s * base[mid], rtol=1e-5)
