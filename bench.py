@@ -192,6 +192,52 @@ def copy_roof(dev: Dev, nbytes: int = 256 << 20, reps: int = 5) -> float:
     return 2 * nbytes * reps / sec
 
 
+GOLDEN_TOKENS = os.path.join(ROOT, "tests", "golden", "llama_3_2_1b_q4_0_seed5.json")
+
+
+def decode_case(runs: int = 3) -> dict:
+    """the synthetic Llama-3.2-1B (seed 5, Q4_0, written as GGUF by the library's
+    own writer and quantizer) through the device decode engine: 32-token prompt, 128 greedy tokens
+    (stop_at_eos=False), `runs` times; tok/s = decode steps / decode time (HIP events around the
+    127 graph-launched decode steps, as the reference's run_ours times its decode steps)."""
+    import shutil
+    import tempfile
+
+    from simd_ml_kernels import llama
+
+    with open(GOLDEN_TOKENS) as f:
+        gold = json.load(f)
+    tmp = tempfile.mkdtemp(prefix="smk_llama_", dir="/tmp")
+    try:
+        t = time.perf_counter()
+        path, prompt = llama.write_synthetic_model(tmp, gold["config"], seed=gold["seed"],
+                                                   n_prompt=len(gold["prompt"]))
+        t_write = time.perf_counter() - t
+        m = llama.Llama(tmp, gguf=path)
+        try:
+            list(m.generate(prompt[:8], 16, stop_at_eos=False))  # warm-up
+            tps, pre = [], []
+            ids = None
+            for _ in range(runs):
+                st = {}
+                ids = list(m.generate(prompt, gold["n_new"], stats=st, stop_at_eos=False))
+                tps.append(st["decode_steps"] / st["decode_s"])
+                pre.append(st["prefill_s"] / st["prefill_tokens"])
+            wb = m.weight_bytes()
+        finally:
+            m.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    tok_s = float(np.median(tps))
+    return {"model": "Llama-3.2-1B architecture, random-init N(0,0.02), Q4_0 (tied token_embd as lm_head)",
+            "prompt_tokens": len(prompt), "new_tokens": gold["n_new"], "decode_tok_s": round(tok_s, 1),
+            "runs_tok_s": [round(v, 1) for v in tps], "ms_per_token": round(1e3 / tok_s, 4),
+            "prefill_ms_per_token": round(1e3 * float(np.median(pre)), 4),
+            "gemv_weight_bytes_per_token": int(wb),
+            "gemv_weight_GBps": round(wb * tok_s / 1e9, 1), "pct_hbm_peak": round(100 * wb * tok_s / PEAK_HBM, 2),
+            "tokens_match_reference_cpu_loop": ids == gold["tokens"], "model_write_s": round(t_write, 1)}
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4_0_8192x2048_hbm_traffic.md")
 
 
@@ -277,6 +323,7 @@ def main() -> int:
             cases[f"q4_0_M{M}_14336x4096"] = quant_case(dev, "q4_0", 14336, 4096, 4, st, wu, args.mode, M=M)
     roof = read_roof(dev)
     copy = copy_roof(dev)
+    decode = decode_case() if args.cases == "all" else None
     sec = head["us"] * 1e-6
     achieved = head["weight_bytes"] / sec
     out = {
@@ -308,6 +355,9 @@ def main() -> int:
         "cases": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                   for k, v in cases.items()},
     }
+    if decode is not None:
+        out["decode_tok_s"] = decode["decode_tok_s"]
+        out["decode"] = decode
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(8192, 2048, args.cpu_seconds)
     print(json.dumps(out))

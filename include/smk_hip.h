@@ -116,6 +116,50 @@ int smk_d_read_roof(const void* src, size_t nbytes, float* sink, int nontemporal
  * and writes exactly nbytes, which also makes it the calibration kernel of the HBM byte counters. */
 int smk_d_copy(void* dst, const void* src, size_t nbytes, void* stream);
 
+/* ─── Device-resident Llama decode ────────────────────────────────────────────
+ * No reference counterpart as a library call: the reference runs this loop in numpy around its
+ * kernels (examples/llama/llama.py:414-505, step/_attention/generate).  Here the whole step
+ * runs on the device from weights uploaded once, with the KV cache in HBM and one HIP graph per
+ * token.  Weight types are ggml ids: 0 F32, 2 Q4_0, 8 Q8_0. */
+typedef struct smk_llama_config {
+    int n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab;
+    int matrix_type;      /* type of every layer matrix (q, k, v, o, gate, up, down) */
+    int embed_type;       /* type of token_embd */
+    int head_type;        /* type of output.weight, or -1: tied to token_embd (llama.py:336-340) */
+    int rope_interleaved; /* 1: pairs (2i, 2i+1) (GGUF, llama.py:387-396); 0: halves (llama.py:169-178) */
+    double rms_eps;
+} smk_llama_config;
+
+/* Tensor ids of smk_llama_set_tensor (GGUF names in comments; layer-wise ids take `layer`). */
+#define SMK_LLAMA_TOKEN_EMBD 0  /* token_embd.weight [vocab, hidden] */
+#define SMK_LLAMA_OUTPUT_NORM 1 /* output_norm.weight [hidden] F32 */
+#define SMK_LLAMA_OUTPUT 2      /* output.weight [vocab, hidden] (only if not tied) */
+#define SMK_LLAMA_ATTN_NORM 3   /* blk.L.attn_norm.weight [hidden] F32 */
+#define SMK_LLAMA_ATTN_Q 4      /* blk.L.attn_q.weight [n_heads*head_dim, hidden] */
+#define SMK_LLAMA_ATTN_K 5      /* blk.L.attn_k.weight [n_kv_heads*head_dim, hidden] */
+#define SMK_LLAMA_ATTN_V 6      /* blk.L.attn_v.weight [n_kv_heads*head_dim, hidden] */
+#define SMK_LLAMA_ATTN_OUTPUT 7 /* blk.L.attn_output.weight [hidden, n_heads*head_dim] */
+#define SMK_LLAMA_FFN_NORM 8    /* blk.L.ffn_norm.weight [hidden] F32 */
+#define SMK_LLAMA_FFN_GATE 9    /* blk.L.ffn_gate.weight [ffn, hidden] */
+#define SMK_LLAMA_FFN_UP 10     /* blk.L.ffn_up.weight [ffn, hidden] */
+#define SMK_LLAMA_FFN_DOWN 11   /* blk.L.ffn_down.weight [hidden, ffn] */
+
+int smk_llama_create(const smk_llama_config* cfg, void** model);
+int smk_llama_destroy(void* model);
+/* Copy one tensor's bytes (GGUF layout, host memory) into the model; nbytes must match. */
+int smk_llama_set_tensor(void* model, int tensor, int layer, const void* host, size_t nbytes);
+/* Empty KV cache for `capacity` positions (llama.py:379-385) and the RoPE tables of those
+ * positions, cos/sin [capacity, head_dim] as rope_cos_sin makes them (llama.py:162-166). */
+int smk_llama_reset(void* model, int capacity, const float* cos_table, const float* sin_table);
+/* One token at the next position (llama.py:414-439); logits: host float [vocab], or NULL to skip
+ * the lm_head (step(token, logits=False)). */
+int smk_llama_step(void* model, int token, float* logits);
+/* Greedy decode from an empty cache (llama.py:481-505 with stop_at_eos=False): n_prompt prompt
+ * steps, then n_new - 1 decode steps, argmax on the device (np.argmax's first-maximum rule);
+ * out: the n_new generated ids; seconds (optional, 2 doubles): prefill and decode time. */
+int smk_llama_generate(void* model, const int* prompt, int n_prompt, int n_new, int* out, double* seconds);
+int smk_llama_info(void* model, int* position, int* capacity, unsigned long long* weight_bytes);
+
 /* Device memory, copies, streams, events and graphs, for callers without their own runtime
  * objects (the tests and bench.py use these; no other framework is loaded with the library). */
 int smk_malloc(void** dptr, size_t nbytes);
@@ -144,6 +188,10 @@ int smk_runtime_version(int* runtime, int* built);
  * workgroup and per-step row unroll (0 = automatic; the last two apply to one row of x),
  * and report the kernel a call would use ("pairs" or "generic"). */
 int smk_set_gemv_tuning(int lanes_per_row, int rows_per_wg, int threads, int unroll);
+/* Diagnostics: 1 (default) sums every Q4_0 row in the reference's SIMD order (q4_0_rows.hpp:
+ * y bit-exact with its AVX2 / AVX-512 tables); 0 selects the free-order kernel, whose y is
+ * within the reference's error bound, for speed comparisons. */
+int smk_set_q4_order(int reference_order);
 const char* smk_gemv_path(int K, const void* Wq);
 
 #ifdef __cplusplus

@@ -66,6 +66,17 @@ def lib() -> ctypes.CDLL:
                                _f32p, ctypes.c_int]
     L.smko_silu.restype = None
     L.smko_silu.argtypes = [_f32p, _f32p, ctypes.c_int]
+    L.smko_gemv_q4_0_simd.restype = None
+    L.smko_gemv_q4_0_simd.argtypes = [ctypes.c_int, ctypes.c_int, _f32p, _u8p, _f32p]
+    for name in ("smko_sgemm_tb_simd", "smko_sgemm_nn_simd"):
+        getattr(L, name).restype = None
+        getattr(L, name).argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float, _f32p, ctypes.c_int,
+                                     _f32p, ctypes.c_int, ctypes.c_float, _f32p, ctypes.c_int]
+    L.smko_fast_exp.restype = ctypes.c_float
+    L.smko_fast_exp.argtypes = [ctypes.c_float]
+    for name in ("smko_silu_simd", "smko_softmax_simd"):
+        getattr(L, name).restype = None
+        getattr(L, name).argtypes = [_f32p, _f32p, ctypes.c_int]
     return L
 
 
@@ -213,6 +224,53 @@ def silu_scalar(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.empty_like(x)
     lib().smko_silu(_p(x, _f32p), _p(y, _f32p), x.size)
+    return y
+
+
+def gemv_q4_0_simd(x: np.ndarray, Wq: np.ndarray, N: int, K: int) -> np.ndarray:
+    """The reference's SIMD-table Q4_0 GEMV order (q4_0_rows.hpp): bit-exact y."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(N, np.float32)
+    lib().smko_gemv_q4_0_simd(N, K, _p(x, _f32p), _p(np.ascontiguousarray(Wq), _u8p), _p(y, _f32p))
+    return y
+
+
+def sgemm_tb_simd(A: np.ndarray, B: np.ndarray, alpha: float = 1.0) -> np.ndarray:
+    """alpha * A @ B.T in the AVX-512 table's few-row order (avx512_gemm_packed.cpp:216-240)."""
+    A = np.ascontiguousarray(A, np.float32)
+    B = np.ascontiguousarray(B, np.float32)
+    M, K = A.shape
+    N = B.shape[0]
+    C = np.zeros((M, N), np.float32)
+    lib().smko_sgemm_tb_simd(M, N, K, alpha, _p(A, _f32p), K, _p(B, _f32p), K, 0.0, _p(C, _f32p), N)
+    return C
+
+
+def sgemm_nn_simd(A: np.ndarray, B: np.ndarray, alpha: float = 1.0) -> np.ndarray:
+    """alpha * A @ B in the AVX2 direct path's order (avx2_gemm_packed.cpp:151-201)."""
+    A = np.ascontiguousarray(A, np.float32)
+    B = np.ascontiguousarray(B, np.float32)
+    M, K = A.shape
+    N = B.shape[1]
+    C = np.zeros((M, N), np.float32)
+    lib().smko_sgemm_nn_simd(M, N, K, alpha, _p(A, _f32p), K, _p(B, _f32p), N, 0.0, _p(C, _f32p), N)
+    return C
+
+
+def silu_simd(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().smko_silu_simd(_p(x, _f32p), _p(y, _f32p), x.size)
+    return y
+
+
+def softmax_simd(x: np.ndarray) -> np.ndarray:
+    """Rows of x through softmax_row_avx2's order (softmax_avx2.cpp:94-186)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    n = x.shape[-1]
+    for r in range(x.size // max(n, 1)):
+        lib().smko_softmax_simd(_p(x.reshape(-1, n)[r], _f32p), _p(y.reshape(-1, n)[r], _f32p), n)
     return y
 
 

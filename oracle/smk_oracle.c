@@ -241,3 +241,191 @@ void smko_gemm_tb(int elem, int M, int N, int K, float alpha, const void* A, int
 void smko_silu(const float* in, float* out, int n) {
     for (int i = 0; i < n; ++i) out[i] = in[i] / (1.0f + expf(-in[i]));
 }
+
+/* ─── The reference's SIMD-path arithmetic orders ───────────────────────────
+ * The AVX2 / AVX-VNNI / AVX512-VNNI tables share one Q4_0 row loop (q4_0_rows.hpp:71-167,
+ * eight rows per group in every unit: q4_0_avx2.cpp:31, q4_0_avxvnni.cpp:28,
+ * q4_0_avx512vnni.cpp:30).  Rows are walked in pairs, one row per 128-bit half of a YMM
+ * register: lane k (0..3) of a row holds the exact integer dot of values {4k..4k+3} (low
+ * nibbles) and {16+4k..16+4k+3} (high nibbles) with x's quants, -8 times x's sum over the
+ * same eight values as its start, and accumulates fma(float(dot), fp16(d)*dx, acc) over the
+ * blocks in order; y = (acc0 + acc2) + (acc1 + acc3) (q4_hsum4).  The last row of an odd N
+ * takes q4_row_single: eight lanes, lane k < 4 over values {4k..4k+3}, lane k >= 4 over
+ * {16+4(k-4)..}; y = hsum4(acc[0..3] + acc[4..7]). */
+static int32_t q4_lane_dot(const uint8_t* qbytes, const int8_t* xb, const int* vals, int nvals) {
+    int32_t s = 0, sx = 0;
+    for (int i = 0; i < nvals; ++i) {
+        const int v = vals[i];
+        const int q = v < 16 ? (qbytes[v] & 0x0f) : (qbytes[v - 16] >> 4);
+        s += q * xb[v];
+        sx += xb[v];
+    }
+    return s - 8 * sx;
+}
+
+void smko_gemv_q4_0_simd(int N, int K, const float* x, const uint8_t* Wq, float* y) {
+    if (N <= 0) return;
+    if (K <= 0) { for (int n = 0; n < N; ++n) y[n] = 0.0f; return; }
+    const int nb = K / 32;
+    int8_t qs[K];
+    float dx[nb];
+    if (!smko_quantize_x_q8(x, K, qs, dx)) {
+        for (int n = 0; n < N; ++n) y[n] = NAN;
+        return;
+    }
+    for (int n = 0; n < N; ++n) {
+        const int single = (N & 1) && n == N - 1;
+        const int lanes = single ? 8 : 4;
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int b = 0; b < nb; ++b) {
+            const uint8_t* blk = Wq + ((size_t)n * nb + b) * 18;
+            const float s = scale_of(blk) * dx[b];
+            for (int k = 0; k < lanes; ++k) {
+                int vals[8], nv = 0;
+                if (!single) {
+                    for (int j = 0; j < 4; ++j) vals[nv++] = 4 * k + j;
+                    for (int j = 0; j < 4; ++j) vals[nv++] = 16 + 4 * k + j;
+                } else {
+                    const int base = k < 4 ? 4 * k : 16 + 4 * (k - 4);
+                    for (int j = 0; j < 4; ++j) vals[nv++] = base + j;
+                }
+                const int32_t d = q4_lane_dot(blk + 2, qs + 32 * b, vals, nv);
+                acc[k] = fmaf((float)d, s, acc[k]);
+            }
+        }
+        if (single)
+            for (int k = 0; k < 4; ++k) acc[k] = acc[k] + acc[k + 4];
+        y[n] = (acc[0] + acc[2]) + (acc[1] + acc[3]);
+    }
+}
+
+/* AVX-512 table, trans_b with a few rows (avx512_gemm_packed.cpp:216-240): per output, two
+ * 16-lane accumulators over steps of 32 (lane l of the first takes p + l, of the second
+ * p + 16 + l; a masked tail step for K % 32), fused multiply-adds; then the 16 sums of the two
+ * accumulators are reduced by halves (lanes i and i + 8, then i and i + 4, then i and i + 2,
+ * then the last two: _mm512_reduce_add_ps); c = c*beta-scaled + alpha * sum. */
+static float reduce16(const float* v) {
+    float t8[8], t4[4], t2[2];
+    for (int i = 0; i < 8; ++i) t8[i] = v[8 + i] + v[i];
+    for (int i = 0; i < 4; ++i) t4[i] = t8[4 + i] + t8[i];
+    t2[0] = t4[0] + t4[2];
+    t2[1] = t4[1] + t4[3];
+    return t2[0] + t2[1];
+}
+
+void smko_sgemm_tb_simd(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,
+                        float beta, float* C, int ldc) {
+    if (M <= 0 || N <= 0 || K < 0) return;
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            float* c = C + (size_t)i * ldc + j;
+            if (beta == 0.0f) *c = 0.0f;
+            else if (beta != 1.0f) *c *= beta;
+        }
+    if (K == 0) return;
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            const float* a = A + (size_t)i * lda;
+            const float* b = B + (size_t)j * ldb;
+            float acc0[16], acc1[16], v[16];
+            for (int l = 0; l < 16; ++l) acc0[l] = acc1[l] = 0.0f;
+            for (int p = 0; p < K; p += 32)
+                for (int l = 0; l < 16; ++l) {
+                    if (p + l < K) acc0[l] = fmaf(a[p + l], b[p + l], acc0[l]);
+                    if (p + 16 + l < K) acc1[l] = fmaf(a[p + 16 + l], b[p + 16 + l], acc1[l]);
+                }
+            for (int l = 0; l < 16; ++l) v[l] = acc0[l] + acc1[l];
+            float* c = C + (size_t)i * ldc + j;
+            *c = fmaf(alpha, reduce16(v), *c);
+        }
+}
+
+/* AVX2 direct path without transposes (avx2_gemm_packed.cpp:151-201, 599-620): per output one
+ * fused multiply-add chain over p in order, then c = fma(acc, alpha, c-prescaled-by-beta). */
+void smko_sgemm_nn_simd(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,
+                        float beta, float* C, int ldc) {
+    if (M <= 0 || N <= 0 || K < 0) return;
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            float* c = C + (size_t)i * ldc + j;
+            if (beta == 0.0f) *c = 0.0f;
+            else if (beta != 1.0f) *c *= beta;
+        }
+    if (K == 0) return;
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            float acc = 0.0f;
+            for (int p = 0; p < K; ++p) acc = fmaf(A[(size_t)i * lda + p], B[(size_t)p * ldb + j], acc);
+            float* c = C + (size_t)i * ldc + j;
+            *c = fmaf(acc, alpha, *c);
+        }
+}
+
+/* fast_exp_avx2 (simd_math.hpp:63-117): clamp to +-88.3762626647949, k = floor(z*log2e + 0.5)
+ * (one fused multiply-add), f = z - k*ln2_hi - k*ln2_lo (two fused steps), a degree-6 Horner
+ * polynomial in fused multiply-adds, times 2^k built from the exponent bits.  min/max keep
+ * the second operand when the first is NaN, as vminps / vmaxps. */
+float smko_fast_exp(float z) {
+    const float hi = 88.3762626647949f, lo = -88.3762626647949f;
+    z = z < hi ? z : hi;
+    z = z > lo ? z : lo;
+    const float kf = floorf(fmaf(z, 1.44269504088896341f, 0.5f));
+    const int ki = (int)kf;
+    float f = fmaf(-kf, 0.693359375f, z);
+    f = fmaf(-kf, -2.12194440e-4f, f);
+    float p = 1.3890048347e-3f;
+    p = fmaf(p, f, 8.3338161260e-3f);
+    p = fmaf(p, f, 4.1666668259e-2f);
+    p = fmaf(p, f, 1.6666667163e-1f);
+    p = fmaf(p, f, 0.5f);
+    p = fmaf(p, f, 1.0f);
+    p = fmaf(p, f, 1.0f);
+    return p * u2f((uint32_t)(ki + 127) << 23);
+}
+
+/* silu_avx2 (silu_avx2.cpp:38-45): x / (1 + fast_exp(-x)), the denominator +inf when -x > 88. */
+void smko_silu_simd(const float* in, float* out, int n) {
+    for (int i = 0; i < n; ++i) {
+        const float x = in[i], nx = -x;
+        float d = 1.0f + smko_fast_exp(nx);
+        if (nx > 88.0f) d = INFINITY;
+        out[i] = x / d;
+    }
+}
+
+/* softmax_row_avx2 (softmax_avx2.cpp:94-186): NaN rows as the scalar kernel; then per full
+ * group of 8 e = fast_exp(x - max) stored as float, its double added to eight running double
+ * sums (lane j of the group into sum j); those eight are added in order (s0+s1+...+s7) to 0;
+ * the last n % 8 values use e = exp(double(x - max)) (glibc) added in order; every output is
+ * then multiplied by float(1 / sum). */
+void smko_softmax_simd(const float* in, float* out, int n) {
+    if (n <= 0) return;
+    float mx = in[0];
+    int bad = 0;
+    for (int i = 0; i < n; ++i) {
+        const uint32_t u = f2u(in[i]);
+        bad |= (u & 0x7fffffffu) > 0x7f800000u || u == 0x7f800000u;
+        if (in[i] > mx) mx = in[i];
+    }
+    if (bad || f2u(mx) == 0xff800000u) {
+        for (int i = 0; i < n; ++i) out[i] = NAN;
+        return;
+    }
+    double lanes[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int j = 0; j < 8; ++j) {
+            const float e = smko_fast_exp(in[i + j] - mx);
+            out[i + j] = e;
+            lanes[j] += (double)e;
+        }
+    double sum = 0.0;
+    sum += lanes[0] + lanes[1] + lanes[2] + lanes[3] + lanes[4] + lanes[5] + lanes[6] + lanes[7];
+    for (; i < n; ++i) {
+        const double e = exp((double)(in[i] - mx));
+        out[i] = (float)e;
+        sum += e;
+    }
+    const float inv = (float)(1.0 / sum);
+    for (int j = 0; j < n; ++j) out[j] *= inv;
+}

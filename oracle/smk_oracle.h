@@ -39,6 +39,16 @@ void smko_gemm_tb(int elem, int M, int N, int K, float alpha, const void* A, int
 
 void smko_silu(const float* in, float* out, int n);
 
+/* The reference's SIMD tables' arithmetic orders (AVX2 / AVX-512; see smk_oracle.c). */
+void smko_gemv_q4_0_simd(int N, int K, const float* x, const uint8_t* Wq, float* y);
+void smko_sgemm_tb_simd(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,
+                        float beta, float* C, int ldc);
+void smko_sgemm_nn_simd(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,
+                        float beta, float* C, int ldc);
+float smko_fast_exp(float z);
+void smko_silu_simd(const float* in, float* out, int n);
+void smko_softmax_simd(const float* in, float* out, int n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,679 @@
+// decoder.hip -- device-resident Llama decode step for gfx950: the per-token loop of
+// examples/llama/llama.py (step :414-439, _attention :398-412, generate :481-505) with every
+// weight, activation and the KV cache in HBM, and one HIP graph per token.
+//
+// Per layer, the step runs (llama.py:428-434):
+//   h = rms_norm(x, attn_norm)                   rms_norm kernel (numpy-exact)
+//   [q|k|v] = h @ [Wq;Wk;Wv]^T                   one GEMV over the three matrices' rows
+//   q, k = rope(q), rope(k); cache[pos] = k, v   rope_kv_kernel
+//   a = attention(q, cache[0..pos])              attention_kernel (one workgroup per head)
+//   x = x + a @ Wo^T                             GEMV with a residual epilogue
+//   h = rms_norm(x, mlp_norm)
+//   [g|u] = h @ [Wgate;Wup]^T                    one GEMV
+//   x = x + (silu(g) * u) @ Wdown^T              silu_mul_kernel, GEMV with residual epilogue
+// then logits = rms_norm(x, norm) @ lm_head^T and the greedy argmax on the device.
+//
+// Rows of a GEMV are independent and the lane split depends on K only, so the fused
+// [q|k|v] and [g|u] products equal the separate per-matrix calls bit for bit.  The position
+// and the token of a step live in device memory (DecodeState, the token array): a captured
+// graph replays unchanged for every position, and generate() runs prompt and decode steps
+// back to back with no host round trip.
+#include "abi_internal.hpp"
+#include "device_common.hpp"
+#include "launch.hpp"
+#include "smk_hip.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace smk {
+namespace {
+
+constexpr int kGgmlF32 = 0, kGgmlQ4_0 = 2, kGgmlQ8_0 = 8;
+constexpr int kMaxCapacity = 32768;  // attention scores of one head live in LDS
+
+struct DecodeState {
+    int pos;       // position of the next step
+    int n_prompt;  // tokens[0, n_prompt) are given; argmax fills the rest
+};
+
+// ─── kernels ────────────────────────────────────────────────────────────────
+
+// x = row `token` of the embedding (llama.py:337 / gguf_reader.py:112-129: d * (q - 8) for
+// Q4_0, d * q for Q8_0, the float32 row for F32; every product is exact in float32).
+__global__ void embed_kernel(const uint8_t* __restrict__ E, int type, int hidden, int vocab,
+                             const int* __restrict__ tokens, const DecodeState* __restrict__ st,
+                             float* __restrict__ x) {
+    int tok = tokens[st->pos];
+    tok = min(max(tok, 0), vocab - 1);  // host checks every token; a bad one must not fault
+    const int nb = hidden >> 5;
+    for (int i = threadIdx.x; i < hidden; i += blockDim.x) {
+        float v;
+        if (type == kGgmlF32) {
+            v = reinterpret_cast<const float*>(E)[static_cast<size_t>(tok) * hidden + i];
+        } else {
+            const int b = i >> 5, j = i & 31;
+            const int bb = type == kGgmlQ4_0 ? kQ4_0Bytes : kQ8_0Bytes;
+            const uint8_t* blk = E + (static_cast<size_t>(tok) * nb + b) * bb;
+            const float d = half_bits_to_float(static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8));
+            int q;
+            if (type == kGgmlQ4_0) {
+                const int byte = blk[2 + (j & 15)];
+                q = (j < 16 ? (byte & 15) : (byte >> 4)) - 8;
+            } else {
+                q = static_cast<int8_t>(blk[2 + j]);
+            }
+            v = d * static_cast<float>(q);
+        }
+        x[i] = v;
+    }
+}
+
+// RoPE of q (in place) and k, and the cache write of k and v at st->pos.  qkv holds n_heads q
+// heads, then n_kv k heads, then n_kv v heads.  Caches: [n_kv, cap, hd] of this layer.
+__global__ void rope_kv_kernel(float* __restrict__ qkv, const float* __restrict__ cos_tab,
+                               const float* __restrict__ sin_tab, int n_heads, int n_kv, int hd, int interleaved,
+                               float* __restrict__ kc, float* __restrict__ vc, int cap,
+                               const DecodeState* __restrict__ st) {
+    const int pos = st->pos;
+    const float* cs = cos_tab + static_cast<size_t>(pos) * hd;
+    const float* sn = sin_tab + static_cast<size_t>(pos) * hd;
+    const int half = hd / 2;
+    const int rot = (n_heads + n_kv) * half;
+    const int total = rot + n_kv * hd;
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < total; t += gridDim.x * blockDim.x) {
+        if (t < rot) {
+            const int head = t / half, i = t - head * half;
+            const float* xr = qkv + static_cast<size_t>(head) * hd;
+            float* dst = head < n_heads ? qkv + static_cast<size_t>(head) * hd
+                                        : kc + (static_cast<size_t>(head - n_heads) * cap + pos) * hd;
+            if (interleaved) {
+                const float a = xr[2 * i], b = xr[2 * i + 1];
+                float o0, o1;
+                rope_pair_interleaved(a, b, cs[i], sn[i], o0, o1);
+                dst[2 * i] = o0;
+                dst[2 * i + 1] = o1;
+            } else {
+                const float lo = xr[i], hi = xr[half + i];
+                float o0, o1;
+                rope_pair_half(lo, hi, cs[i], sn[i], cs[half + i], sn[half + i], o0, o1);
+                dst[i] = o0;
+                dst[half + i] = o1;
+            }
+        } else {
+            const int u = t - rot, g = u / hd, d = u - g * hd;
+            vc[(static_cast<size_t>(g) * cap + pos) * hd + d] = qkv[static_cast<size_t>(n_heads + n_kv) * hd + u];
+        }
+    }
+}
+
+// Grouped-query attention of one query head over positions 0..pos (llama.py:398-412), in the
+// arithmetic order of the reference's SIMD tables, so that every score, probability and output
+// equals the reference's bit for bit:
+//   scores = sk.sgemm(q, K, alpha=scale, trans_b=True): the AVX-512 few-row dot
+//     (avx512_gemm_packed.cpp:216-240): 16 lanes per dot, lane l accumulating products
+//     p = l, l+32, ... and 16+l, 48+l, ... in two fused chains, the two chains added, the 16
+//     sums reduced by halves (lanes i and i+8, i and i+4, i and i+2, then the pair), times scale;
+//   p = sk.softmax(scores): softmax_row_avx2's order (the exp of simd_math.hpp on full groups
+//     of 8, eight running double sums, a double exp on the last n % 8);
+//   out = sk.sgemm(p, V): the AVX2 direct product (avx2_gemm_packed.cpp:151-201), one fused
+//     chain over the positions in order per output.
+// One workgroup of 256 threads per head; scores in LDS.
+constexpr int kAttnThreads = 256;
+
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __restrict__ q_all,
+                                                                 const float* __restrict__ kc,
+                                                                 const float* __restrict__ vc, int n_heads, int n_kv,
+                                                                 int hd, int cap, float scale,
+                                                                 const DecodeState* __restrict__ st,
+                                                                 float* __restrict__ out) {
+    extern __shared__ float sc[];  // T scores, then probabilities
+    __shared__ float qs[256];
+    __shared__ float red_f[kAttnThreads / kWave];
+    __shared__ int red_i[kAttnThreads / kWave];
+    __shared__ double lane_sum[8];
+    __shared__ float tail_d[8];
+    __shared__ float inv_s;
+    const int head = blockIdx.x;
+    const int g = head / (n_heads / n_kv);
+    const int T = st->pos + 1;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    constexpr int kWaves = kAttnThreads / kWave;
+    for (int d = threadIdx.x; d < hd; d += kAttnThreads) qs[d] = q_all[static_cast<size_t>(head) * hd + d];
+    __syncthreads();
+    const float* K = kc + static_cast<size_t>(g) * cap * hd;
+    const float* V = vc + static_cast<size_t>(g) * cap * hd;
+    // Scores: 16 lanes per position.
+    const int l = threadIdx.x & 15;
+    for (int t0 = 0; t0 < T; t0 += kAttnThreads / 16) {
+        const int t = t0 + static_cast<int>(threadIdx.x >> 4);
+        const int tt = min(t, T - 1);
+        const float* kr = K + static_cast<size_t>(tt) * hd;
+        float a0 = 0.0f, a1 = 0.0f;
+        for (int p = 0; p < hd; p += 32) {
+            if (p + l < hd) a0 = fmaf(qs[p + l], kr[p + l], a0);
+            if (p + 16 + l < hd) a1 = fmaf(qs[p + 16 + l], kr[p + 16 + l], a1);
+        }
+        float v = a0 + a1;
+        v = v + __shfl_xor(v, 8, 16);
+        v = v + __shfl_xor(v, 4, 16);
+        v = v + __shfl_xor(v, 2, 16);
+        v = v + __shfl_xor(v, 1, 16);
+        if (l == 0 && t < T) sc[t] = scale * v;
+    }
+    __syncthreads();
+    // Softmax over the T scores.
+    float mx = -__builtin_inff();
+    int nonfinite = 0;
+    for (int t = threadIdx.x; t < T; t += kAttnThreads) {
+        const uint32_t u = __float_as_uint(sc[t]);
+        nonfinite |= (u & 0x7fffffffu) > 0x7f800000u || u == 0x7f800000u;
+        mx = fmaxf(mx, sc[t]);
+    }
+    mx = group_max<kWave>(mx);
+    nonfinite = group_sum_int<kWave>(nonfinite);
+    if (lane == 0) {
+        red_f[wave] = mx;
+        red_i[wave] = nonfinite;
+    }
+    __syncthreads();
+    mx = red_f[0];
+    nonfinite = red_i[0];
+    for (int w = 1; w < kWaves; ++w) {
+        mx = fmaxf(mx, red_f[w]);
+        nonfinite |= red_i[w];
+    }
+    const bool nan_row = nonfinite || __float_as_uint(mx) == 0xff800000u;
+    const int n8 = T - T % 8;
+    for (int t = threadIdx.x; t < T; t += kAttnThreads) {
+        const float dd = sc[t] - mx;
+        if (t >= n8) tail_d[t - n8] = dd;
+        sc[t] = t < n8 ? exp_cody_waite(dd) : static_cast<float>(exp(static_cast<double>(dd)));
+    }
+    __syncthreads();
+    if (threadIdx.x < 8) {
+        double acc = 0.0;
+        for (int t = threadIdx.x; t < n8; t += 8) acc = acc + static_cast<double>(sc[t]);
+        lane_sum[threadIdx.x] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double tsum = lane_sum[0];
+        for (int k = 1; k < 8; ++k) tsum = tsum + lane_sum[k];
+        double sum = 0.0 + tsum;
+        for (int t = 0; t < T - n8; ++t) sum = sum + exp(static_cast<double>(tail_d[t]));
+        inv_s = static_cast<float>(1.0 / sum);
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    for (int t = threadIdx.x; t < T; t += kAttnThreads) sc[t] = nan_row ? __builtin_nanf("") : sc[t] * inv;
+    __syncthreads();
+    // out[d] = one fused chain over the positions in order.
+    for (int d = threadIdx.x; d < hd; d += kAttnThreads) {
+        float acc = 0.0f;
+        for (int t = 0; t < T; ++t) acc = fmaf(sc[t], V[static_cast<size_t>(t) * hd + d], acc);
+        out[static_cast<size_t>(head) * hd + d] = acc;
+    }
+}
+
+// m = silu(g) * u (llama.py:434: sk.silu(gate) * up, two float32 results multiplied), SiLU as
+// the reference's SIMD tables compute it.
+__global__ void silu_mul_kernel(const float* __restrict__ gu, int ffn, float* __restrict__ m) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < ffn; i += gridDim.x * blockDim.x)
+        m[i] = silu_ref(gu[i]) * gu[ffn + i];
+}
+
+// np.argmax semantics: the first index of the maximum; a NaN counts as the maximum (the first
+// NaN wins).
+__device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
+    const bool an = a != a, bn = b != b;
+    if (an || bn) return an && (!bn || ia < ib);
+    return a > b || (a == b && ia < ib);
+}
+
+// Greedy next token from the logits, then the position advances.  tokens[pos + 1] is written
+// only past the given prompt.
+constexpr int kArgmaxThreads = 1024;
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, int n,
+                                                                int* __restrict__ tokens, int cap,
+                                                                DecodeState* __restrict__ st) {
+    __shared__ float bv[kArgmaxThreads / kWave];
+    __shared__ int bi[kArgmaxThreads / kWave];
+    float v = -__builtin_inff();
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += kArgmaxThreads) {
+        const float c = logits[i];
+        if (better(c, i, v, idx)) {
+            v = c;
+            idx = i;
+        }
+    }
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off, kWave);
+        const int oi = __shfl_xor(idx, off, kWave);
+        if (better(ov, oi, v, idx)) {
+            v = ov;
+            idx = oi;
+        }
+    }
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    if (lane == 0) {
+        bv[wave] = v;
+        bi[wave] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kArgmaxThreads / kWave; ++w)
+            if (better(bv[w], bi[w], v, idx)) {
+                v = bv[w];
+                idx = bi[w];
+            }
+        if (idx < 0 || idx >= n) idx = 0;  // n == 0 cannot happen (vocab > 0)
+        const int p = st->pos;
+        if (p + 1 >= st->n_prompt && p + 1 <= cap) tokens[p + 1] = idx;
+        st->pos = p + 1;
+    }
+}
+
+__global__ void advance_kernel(DecodeState* st) {
+    if (threadIdx.x == 0) st->pos = st->pos + 1;
+}
+
+// ─── the model ──────────────────────────────────────────────────────────────
+
+int type_block_bytes(int type) { return type == kGgmlQ4_0 ? kQ4_0Bytes : type == kGgmlQ8_0 ? kQ8_0Bytes : 0; }
+
+size_t matrix_bytes(int type, int rows, int cols) {
+    if (type == kGgmlF32) return static_cast<size_t>(rows) * cols * 4;
+    return static_cast<size_t>(rows) * (cols / 32) * type_block_bytes(type);
+}
+
+struct Mat {
+    uint8_t* p = nullptr;
+    int type = kGgmlQ4_0, rows = 0, cols = 0;
+    size_t bytes() const { return matrix_bytes(type, rows, cols); }
+    size_t row_bytes() const { return rows ? bytes() / rows : 0; }
+};
+
+struct Layer {
+    float* attn_norm = nullptr;
+    float* ffn_norm = nullptr;
+    Mat qkv, o, gateup, down;
+};
+
+struct Model {
+    smk_llama_config cfg{};
+    hipStream_t stream = nullptr;
+    Mat embed, head;
+    bool tied = true;
+    float* out_norm = nullptr;
+    std::vector<Layer> layers;
+    std::vector<void*> allocs;
+    // activations
+    float *x = nullptr, *h = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *m = nullptr,
+          *logits = nullptr;
+    DecodeState* st = nullptr;
+    int* host_pinned = nullptr;  // staging for tokens and state
+    // per capacity
+    int capacity = 0;
+    int pos = 0;
+    int* tokens = nullptr;
+    float *kc = nullptr, *vc = nullptr, *cos_tab = nullptr, *sin_tab = nullptr;
+    hipGraphExec_t g_logits = nullptr, g_plain = nullptr;
+    std::vector<unsigned> loaded;  // bit per tensor per layer
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    uint64_t weight_bytes = 0;
+
+    int q_rows() const { return cfg.n_heads * cfg.head_dim; }
+    int kv_rows() const { return cfg.n_kv_heads * cfg.head_dim; }
+};
+
+hipError_t dalloc(Model& md, void** p, size_t bytes) {
+    *p = nullptr;
+    const hipError_t e = hipMalloc(p, std::max<size_t>(bytes, 256));
+    if (e == hipSuccess) md.allocs.push_back(*p);
+    return e;
+}
+
+void free_capacity(Model& md) {
+    if (md.g_logits) (void)hipGraphExecDestroy(md.g_logits);
+    if (md.g_plain) (void)hipGraphExecDestroy(md.g_plain);
+    md.g_logits = md.g_plain = nullptr;
+    for (void* p : {static_cast<void*>(md.tokens), static_cast<void*>(md.kc), static_cast<void*>(md.vc),
+                    static_cast<void*>(md.cos_tab), static_cast<void*>(md.sin_tab)})
+        if (p) (void)hipFree(p);
+    md.tokens = nullptr;
+    md.kc = md.vc = md.cos_tab = md.sin_tab = nullptr;
+    md.capacity = 0;
+}
+
+hipError_t gemv(const Mat& W, const float* x, float* y, bool accumulate, hipStream_t s) {
+    if (W.type == kGgmlF32)
+        return gemm_tb(0, 1, W.rows, W.cols, 1.0f, x, W.cols, W.p, W.cols, accumulate ? 1.0f : 0.0f, y, W.rows, s);
+    GemvTuning t;
+    t.accumulate = accumulate ? 1 : 0;
+    return gemv_quant(type_block_bytes(W.type), 1, W.rows, W.cols, x, W.cols, W.p, y, W.rows, s, &t);
+}
+
+// Enqueue one decode step (the body every graph captures).
+hipError_t enqueue_step(Model& md, bool with_logits) {
+    const smk_llama_config& c = md.cfg;
+    hipStream_t s = md.stream;
+    const int nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
+    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, md.embed.p, md.embed.type, c.hidden, c.vocab,
+                       md.tokens, md.st, md.x);
+    if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    const size_t layer_kv = static_cast<size_t>(nkv) * md.capacity * hd;
+    const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(hd)));
+    const int rope_total = (nh + nkv) * (hd / 2) + nkv * hd;
+    for (int l = 0; l < c.n_layers; ++l) {
+        const Layer& L = md.layers[l];
+        float* kc = md.kc + l * layer_kv;
+        float* vc = md.vc + l * layer_kv;
+        hipError_t e = rms_norm(md.x, L.attn_norm, md.h, 1, c.hidden, c.rms_eps, s);
+        if (e == hipSuccess) e = gemv(L.qkv, md.h, md.qkv, false, s);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(rope_kv_kernel, dim3((rope_total + 255) / 256), dim3(256), 0, s, md.qkv, md.cos_tab,
+                           md.sin_tab, nh, nkv, hd, c.rope_interleaved, kc, vc, md.capacity, md.st);
+        hipLaunchKernelGGL(attention_kernel, dim3(nh), dim3(kAttnThreads), static_cast<size_t>(md.capacity) * 4, s,
+                           md.qkv, kc, vc, nh, nkv, hd, md.capacity, scale, md.st, md.attn);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        e = gemv(L.o, md.attn, md.x, true, s);
+        if (e == hipSuccess) e = rms_norm(md.x, L.ffn_norm, md.h, 1, c.hidden, c.rms_eps, s);
+        if (e == hipSuccess) e = gemv(L.gateup, md.h, md.gu, false, s);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(silu_mul_kernel, dim3((c.ffn + 255) / 256), dim3(256), 0, s, md.gu, c.ffn, md.m);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if ((e = gemv(L.down, md.m, md.x, true, s)) != hipSuccess) return e;
+    }
+    if (!with_logits) {
+        hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, s, md.st);
+        return hipGetLastError();
+    }
+    hipError_t e = rms_norm(md.x, md.out_norm, md.h, 1, c.hidden, c.rms_eps, s);
+    if (e == hipSuccess) e = gemv(md.head, md.h, md.logits, false, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, md.logits, c.vocab, md.tokens,
+                       md.capacity, md.st);
+    return hipGetLastError();
+}
+
+hipError_t capture(Model& md, bool with_logits, hipGraphExec_t* out) {
+    hipError_t e = hipStreamBeginCapture(md.stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return e;
+    const hipError_t body = enqueue_step(md, with_logits);
+    hipGraph_t graph = nullptr;
+    e = hipStreamEndCapture(md.stream, &graph);
+    if (body != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return body;
+    }
+    if (e != hipSuccess) return e;
+    e = hipGraphInstantiate(out, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    return e;
+}
+
+// Tensor ids of smk_llama_set_tensor.
+enum { T_EMBD = 0, T_OUT_NORM, T_OUTPUT, T_ATTN_NORM, T_Q, T_K, T_V, T_O, T_FFN_NORM, T_GATE, T_UP, T_DOWN, T_COUNT };
+
+bool all_loaded(const Model& md, std::string* missing) {
+    const int L = md.cfg.n_layers;
+    if (!(md.loaded[0] & (1u << T_EMBD))) return *missing = "token_embd", false;
+    if (!(md.loaded[0] & (1u << T_OUT_NORM))) return *missing = "output_norm", false;
+    if (!md.tied && !(md.loaded[0] & (1u << T_OUTPUT))) return *missing = "output", false;
+    for (int l = 0; l < L; ++l)
+        for (int t = T_ATTN_NORM; t < T_COUNT; ++t)
+            if (!(md.loaded[1 + l] & (1u << t))) return *missing = "layer " + std::to_string(l) + " tensor " + std::to_string(t), false;
+    return true;
+}
+
+}  // namespace
+}  // namespace smk
+
+using namespace smk;
+using namespace smk::abi;
+
+extern "C" {
+
+int smk_llama_create(const smk_llama_config* cfg, void** model) {
+    if (!cfg || !model) return fail(SMK_ERR_ARGUMENT, "null argument");
+    *model = nullptr;
+    const smk_llama_config& c = *cfg;
+    if (c.n_layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 || c.ffn <= 0 ||
+        c.vocab <= 0)
+        return fail(SMK_ERR_ARGUMENT, "every dimension must be positive");
+    if (c.n_heads % c.n_kv_heads) return fail(SMK_ERR_ARGUMENT, "n_heads must be a multiple of n_kv_heads");
+    if (c.head_dim % 2 || c.head_dim > 256) return fail(SMK_ERR_ARGUMENT, "head_dim must be even and <= 256");
+    if (c.hidden % 32 || c.ffn % 32 || (c.n_heads * c.head_dim) % 32)
+        return fail(SMK_ERR_ARGUMENT, "hidden, ffn and n_heads*head_dim must be multiples of 32");
+    for (int t : {c.matrix_type, c.embed_type})
+        if (t != kGgmlF32 && t != kGgmlQ4_0 && t != kGgmlQ8_0)
+            return fail(SMK_ERR_ARGUMENT, "weight types: 0 (F32), 2 (Q4_0) or 8 (Q8_0)");
+    if (c.head_type != -1 && c.head_type != kGgmlF32 && c.head_type != kGgmlQ4_0 && c.head_type != kGgmlQ8_0)
+        return fail(SMK_ERR_ARGUMENT, "head_type: -1 (tied), 0, 2 or 8");
+    if (const int rc = use_device()) return rc;
+    auto* md = new Model();
+    md->cfg = c;
+    md->tied = c.head_type == -1;
+    md->loaded.assign(1 + c.n_layers, 0u);
+    auto cleanup = [&](hipError_t e, const char* what) {
+        for (void* p : md->allocs) (void)hipFree(p);
+        if (md->stream) (void)hipStreamDestroy(md->stream);
+        if (md->host_pinned) (void)hipHostFree(md->host_pinned);
+        for (hipEvent_t& ev : md->ev)
+            if (ev) (void)hipEventDestroy(ev);
+        delete md;
+        return hip_fail(e, what);
+    };
+    hipError_t e = hipStreamCreateWithFlags(&md->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return cleanup(e, "stream");
+    for (hipEvent_t& ev : md->ev)
+        if ((e = hipEventCreate(&ev)) != hipSuccess) return cleanup(e, "event");
+    if ((e = hipHostMalloc(reinterpret_cast<void**>(&md->host_pinned), 4096, hipHostMallocDefault)) != hipSuccess)
+        return cleanup(e, "pinned staging");
+    const int qkv_rows = md->q_rows() + 2 * md->kv_rows();
+    md->embed = {nullptr, c.embed_type, c.vocab, c.hidden};
+    md->head = md->tied ? md->embed : Mat{nullptr, c.head_type, c.vocab, c.hidden};
+    struct Want { void** p; size_t bytes; };
+    std::vector<Want> want = {
+        {reinterpret_cast<void**>(&md->embed.p), md->embed.bytes()},
+        {reinterpret_cast<void**>(&md->out_norm), static_cast<size_t>(c.hidden) * 4},
+        {reinterpret_cast<void**>(&md->x), static_cast<size_t>(c.hidden) * 4},
+        {reinterpret_cast<void**>(&md->h), static_cast<size_t>(std::max(c.hidden, md->q_rows())) * 4},
+        {reinterpret_cast<void**>(&md->qkv), static_cast<size_t>(qkv_rows) * 4},
+        {reinterpret_cast<void**>(&md->attn), static_cast<size_t>(md->q_rows()) * 4},
+        {reinterpret_cast<void**>(&md->gu), static_cast<size_t>(2 * c.ffn) * 4},
+        {reinterpret_cast<void**>(&md->m), static_cast<size_t>(c.ffn) * 4},
+        {reinterpret_cast<void**>(&md->logits), static_cast<size_t>(c.vocab) * 4},
+        {reinterpret_cast<void**>(&md->st), sizeof(DecodeState)},
+    };
+    if (!md->tied) want.push_back({reinterpret_cast<void**>(&md->head.p), md->head.bytes()});
+    md->layers.resize(c.n_layers);
+    for (Layer& L : md->layers) {
+        L.qkv = {nullptr, c.matrix_type, qkv_rows, c.hidden};
+        L.o = {nullptr, c.matrix_type, c.hidden, md->q_rows()};
+        L.gateup = {nullptr, c.matrix_type, 2 * c.ffn, c.hidden};
+        L.down = {nullptr, c.matrix_type, c.hidden, c.ffn};
+        want.push_back({reinterpret_cast<void**>(&L.attn_norm), static_cast<size_t>(c.hidden) * 4});
+        want.push_back({reinterpret_cast<void**>(&L.ffn_norm), static_cast<size_t>(c.hidden) * 4});
+        for (Mat* M : {&L.qkv, &L.o, &L.gateup, &L.down}) want.push_back({reinterpret_cast<void**>(&M->p), M->bytes()});
+    }
+    for (const Want& w : want)
+        if ((e = dalloc(*md, w.p, w.bytes)) != hipSuccess) return cleanup(e, "model allocation");
+    if (md->tied) md->head = md->embed;
+    md->weight_bytes = md->head.bytes();
+    for (const Layer& L : md->layers) md->weight_bytes += L.qkv.bytes() + L.o.bytes() + L.gateup.bytes() + L.down.bytes();
+    *model = md;
+    return ok();
+}
+
+int smk_llama_destroy(void* model) {
+    if (!model) return ok();
+    auto* md = static_cast<Model*>(model);
+    if (const int rc = use_device()) return rc;
+    (void)hipStreamSynchronize(md->stream);
+    free_capacity(*md);
+    for (void* p : md->allocs) (void)hipFree(p);
+    for (hipEvent_t& ev : md->ev)
+        if (ev) (void)hipEventDestroy(ev);
+    if (md->host_pinned) (void)hipHostFree(md->host_pinned);
+    (void)hipStreamDestroy(md->stream);
+    delete md;
+    return ok();
+}
+
+int smk_llama_set_tensor(void* model, int tensor, int layer, const void* host, size_t nbytes) {
+    if (!model || !host) return fail(SMK_ERR_ARGUMENT, "null argument");
+    auto* md = static_cast<Model*>(model);
+    const smk_llama_config& c = md->cfg;
+    const bool per_layer = tensor >= T_ATTN_NORM && tensor < T_COUNT;
+    if (tensor < 0 || tensor >= T_COUNT) return fail(SMK_ERR_ARGUMENT, "unknown tensor id");
+    if (per_layer && (layer < 0 || layer >= c.n_layers)) return fail(SMK_ERR_ARGUMENT, "layer out of range");
+    if (tensor == T_OUTPUT && md->tied) return fail(SMK_ERR_ARGUMENT, "output.weight given but head_type is -1 (tied)");
+    if (const int rc = use_device()) return rc;
+    void* dst = nullptr;
+    size_t want = 0;
+    if (tensor == T_EMBD) {
+        dst = md->embed.p;
+        want = md->embed.bytes();
+    } else if (tensor == T_OUT_NORM) {
+        dst = md->out_norm;
+        want = static_cast<size_t>(c.hidden) * 4;
+    } else if (tensor == T_OUTPUT) {
+        dst = md->head.p;
+        want = md->head.bytes();
+    } else {
+        Layer& L = md->layers[layer];
+        const int qr = md->q_rows(), kr = md->kv_rows();
+        switch (tensor) {
+            case T_ATTN_NORM: dst = L.attn_norm; want = static_cast<size_t>(c.hidden) * 4; break;
+            case T_FFN_NORM: dst = L.ffn_norm; want = static_cast<size_t>(c.hidden) * 4; break;
+            case T_Q: dst = L.qkv.p; want = static_cast<size_t>(qr) * L.qkv.row_bytes(); break;
+            case T_K: dst = L.qkv.p + static_cast<size_t>(qr) * L.qkv.row_bytes(); want = static_cast<size_t>(kr) * L.qkv.row_bytes(); break;
+            case T_V: dst = L.qkv.p + static_cast<size_t>(qr + kr) * L.qkv.row_bytes(); want = static_cast<size_t>(kr) * L.qkv.row_bytes(); break;
+            case T_O: dst = L.o.p; want = L.o.bytes(); break;
+            case T_GATE: dst = L.gateup.p; want = static_cast<size_t>(c.ffn) * L.gateup.row_bytes(); break;
+            case T_UP: dst = L.gateup.p + static_cast<size_t>(c.ffn) * L.gateup.row_bytes(); want = static_cast<size_t>(c.ffn) * L.gateup.row_bytes(); break;
+            case T_DOWN: dst = L.down.p; want = L.down.bytes(); break;
+        }
+    }
+    if (nbytes != want)
+        return fail(SMK_ERR_ARGUMENT, "tensor " + std::to_string(tensor) + ": " + std::to_string(nbytes) +
+                                          " bytes given, " + std::to_string(want) + " expected for its shape and type");
+    SMK_HIP(hipMemcpy(dst, host, nbytes, hipMemcpyHostToDevice), "tensor upload");
+    md->loaded[per_layer ? 1 + layer : 0] |= 1u << tensor;
+    return ok();
+}
+
+int smk_llama_reset(void* model, int capacity, const float* cos_table, const float* sin_table) {
+    if (!model || !cos_table || !sin_table) return fail(SMK_ERR_ARGUMENT, "null argument");
+    auto* md = static_cast<Model*>(model);
+    if (capacity <= 0 || capacity > kMaxCapacity)
+        return fail(SMK_ERR_ARGUMENT, "capacity must be in [1, " + std::to_string(kMaxCapacity) + "]");
+    std::string missing;
+    if (!all_loaded(*md, &missing)) return fail(SMK_ERR_ARGUMENT, "tensor not loaded: " + missing);
+    if (const int rc = use_device()) return rc;
+    SMK_HIP(hipStreamSynchronize(md->stream), "synchronize");
+    const smk_llama_config& c = md->cfg;
+    const size_t kv = static_cast<size_t>(c.n_layers) * c.n_kv_heads * capacity * c.head_dim * 4;
+    const size_t tab = static_cast<size_t>(capacity) * c.head_dim * 4;
+    if (capacity != md->capacity) {
+        free_capacity(*md);
+        SMK_HIP(hipMalloc(reinterpret_cast<void**>(&md->tokens), static_cast<size_t>(capacity + 1) * 4), "tokens");
+        SMK_HIP(hipMalloc(reinterpret_cast<void**>(&md->kc), kv), "k cache");
+        SMK_HIP(hipMalloc(reinterpret_cast<void**>(&md->vc), kv), "v cache");
+        SMK_HIP(hipMalloc(reinterpret_cast<void**>(&md->cos_tab), tab), "cos table");
+        SMK_HIP(hipMalloc(reinterpret_cast<void**>(&md->sin_tab), tab), "sin table");
+        md->capacity = capacity;
+    }
+    SMK_HIP(hipMemsetAsync(md->kc, 0, kv, md->stream), "k cache clear");
+    SMK_HIP(hipMemsetAsync(md->vc, 0, kv, md->stream), "v cache clear");
+    SMK_HIP(hipMemsetAsync(md->tokens, 0, static_cast<size_t>(capacity + 1) * 4, md->stream), "tokens clear");
+    SMK_HIP(hipMemcpyAsync(md->cos_tab, cos_table, tab, hipMemcpyHostToDevice, md->stream), "cos upload");
+    SMK_HIP(hipMemcpyAsync(md->sin_tab, sin_table, tab, hipMemcpyHostToDevice, md->stream), "sin upload");
+    md->host_pinned[0] = 0;
+    md->host_pinned[1] = 0;
+    SMK_HIP(hipMemcpyAsync(md->st, md->host_pinned, sizeof(DecodeState), hipMemcpyHostToDevice, md->stream), "state");
+    SMK_HIP(hipStreamSynchronize(md->stream), "reset");
+    md->pos = 0;
+    if (!md->g_logits) {
+        SMK_HIP(allow_lds(attention_kernel, static_cast<size_t>(capacity) * 4), "attention LDS");
+        SMK_HIP(capture(*md, true, &md->g_logits), "capture step");
+        SMK_HIP(capture(*md, false, &md->g_plain), "capture step (no logits)");
+    }
+    return ok();
+}
+
+int smk_llama_step(void* model, int token, float* logits) {
+    if (!model) return fail(SMK_ERR_ARGUMENT, "null model");
+    auto* md = static_cast<Model*>(model);
+    if (!md->capacity) return fail(SMK_ERR_ARGUMENT, "call smk_llama_reset first");
+    if (md->pos >= md->capacity)
+        return fail(SMK_ERR_ARGUMENT, "KV cache full (" + std::to_string(md->capacity) + " positions)");
+    if (token < 0 || token >= md->cfg.vocab) return fail(SMK_ERR_ARGUMENT, "token out of range");
+    if (const int rc = use_device()) return rc;
+    md->host_pinned[2] = token;
+    SMK_HIP(hipMemcpyAsync(md->tokens + md->pos, md->host_pinned + 2, 4, hipMemcpyHostToDevice, md->stream), "token");
+    SMK_HIP(hipGraphLaunch(logits ? md->g_logits : md->g_plain, md->stream), "step graph");
+    if (logits)
+        SMK_HIP(hipMemcpyAsync(logits, md->logits, static_cast<size_t>(md->cfg.vocab) * 4, hipMemcpyDeviceToHost,
+                               md->stream),
+                "logits download");
+    SMK_HIP(hipStreamSynchronize(md->stream), "step");
+    ++md->pos;
+    return ok();
+}
+
+int smk_llama_generate(void* model, const int* prompt, int n_prompt, int n_new, int* out, double* seconds) {
+    if (!model || !prompt || !out) return fail(SMK_ERR_ARGUMENT, "null argument");
+    auto* md = static_cast<Model*>(model);
+    if (n_prompt <= 0 || n_new <= 0) return fail(SMK_ERR_ARGUMENT, "n_prompt and n_new must be positive");
+    if (md->pos != 0) return fail(SMK_ERR_ARGUMENT, "generate starts from an empty cache: call smk_llama_reset");
+    const int steps = n_prompt + n_new - 1;
+    if (steps > md->capacity) return fail(SMK_ERR_ARGUMENT, "capacity < n_prompt + n_new - 1");
+    for (int i = 0; i < n_prompt; ++i)
+        if (prompt[i] < 0 || prompt[i] >= md->cfg.vocab) return fail(SMK_ERR_ARGUMENT, "prompt token out of range");
+    if (const int rc = use_device()) return rc;
+    SMK_HIP(hipMemcpy(md->tokens, prompt, static_cast<size_t>(n_prompt) * 4, hipMemcpyHostToDevice), "prompt");
+    md->host_pinned[0] = 0;
+    md->host_pinned[1] = n_prompt;
+    SMK_HIP(hipMemcpyAsync(md->st, md->host_pinned, sizeof(DecodeState), hipMemcpyHostToDevice, md->stream), "state");
+    SMK_HIP(hipEventRecord(md->ev[0], md->stream), "event");
+    for (int i = 0; i < n_prompt; ++i) SMK_HIP(hipGraphLaunch(md->g_logits, md->stream), "prefill graph");
+    SMK_HIP(hipEventRecord(md->ev[1], md->stream), "event");
+    for (int i = 0; i < n_new - 1; ++i) SMK_HIP(hipGraphLaunch(md->g_logits, md->stream), "decode graph");
+    SMK_HIP(hipEventRecord(md->ev[2], md->stream), "event");
+    SMK_HIP(hipMemcpyAsync(out, md->tokens + n_prompt, static_cast<size_t>(n_new) * 4, hipMemcpyDeviceToHost,
+                           md->stream),
+            "tokens download");
+    SMK_HIP(hipStreamSynchronize(md->stream), "generate");
+    md->pos = steps;
+    // Back to the step() convention: the given-token count is 0 again.
+    md->host_pinned[0] = steps;
+    md->host_pinned[1] = 0;
+    SMK_HIP(hipMemcpy(md->st, md->host_pinned, sizeof(DecodeState), hipMemcpyHostToDevice), "state");
+    if (seconds) {
+        float a = 0.0f, b = 0.0f;
+        SMK_HIP(hipEventElapsedTime(&a, md->ev[0], md->ev[1]), "elapsed");
+        SMK_HIP(hipEventElapsedTime(&b, md->ev[1], md->ev[2]), "elapsed");
+        seconds[0] = a * 1e-3;
+        seconds[1] = b * 1e-3;
+    }
+    return ok();
+}
+
+int smk_llama_info(void* model, int* position, int* capacity, unsigned long long* weight_bytes) {
+    if (!model) return fail(SMK_ERR_ARGUMENT, "null model");
+    auto* md = static_cast<Model*>(model);
+    if (position) *position = md->pos;
+    if (capacity) *capacity = md->capacity;
+    if (weight_bytes) *weight_bytes = md->weight_bytes;
+    return ok();
+}
+
+}  // extern "C"

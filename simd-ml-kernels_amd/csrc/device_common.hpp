@@ -120,4 +120,54 @@ __device__ __forceinline__ int round_half_away(float v) {
     return static_cast<int>(t) + (r >= 0.5f ? 1 : 0) - (r <= -0.5f ? 1 : 0);
 }
 
+// The reference's vectorised exp (simd_math.hpp:63-117, used by its SiLU and softmax): clamp
+// to +-88.3762626647949 (a NaN becomes the bound, as vminps/vmaxps return their second
+// operand), k = floor(z*log2e + 0.5) with one fused multiply-add, Cody-Waite reduction
+// f = z - k*ln2_hi - k*ln2_lo in two fused steps, the Cephes degree-6 polynomial by fused
+// Horner steps, times 2^k assembled in the exponent field.  Same operations, same roundings:
+// bit-exact with the reference's SIMD tables.
+__device__ __forceinline__ float exp_cody_waite(float z) {
+    const float hi = 88.3762626647949f, lo = -88.3762626647949f;
+    z = z < hi ? z : hi;
+    z = z > lo ? z : lo;
+    const float kf = floorf(fmaf(z, 1.44269504088896341f, 0.5f));
+    const int ki = static_cast<int>(kf);
+    float f = fmaf(-kf, 0.693359375f, z);
+    f = fmaf(-kf, -2.12194440e-4f, f);
+    float p = 1.3890048347e-3f;
+    p = fmaf(p, f, 8.3338161260e-3f);
+    p = fmaf(p, f, 4.1666668259e-2f);
+    p = fmaf(p, f, 1.6666667163e-1f);
+    p = fmaf(p, f, 0.5f);
+    p = fmaf(p, f, 1.0f);
+    p = fmaf(p, f, 1.0f);
+    return p * __uint_as_float(static_cast<uint32_t>(ki + 127) << 23);
+}
+
+// SiLU as the reference's SIMD tables compute it (silu_avx2.cpp:38-45): x / (1 + exp(-x)) with
+// the exp above and an IEEE division; the denominator is +inf when -x > 88 (so the result is
+// -0 there and SiLU(-inf) is NaN).
+__device__ __forceinline__ float silu_ref(float x) {
+    const float nx = -x;
+    float d = 1.0f + exp_cody_waite(nx);
+    if (nx > 88.0f) d = __builtin_inff();
+    return x / d;
+}
+
+// RoPE of one pair, every product and sum rounded on its own (numpy's order):
+// interleaved (llama.py:387-396): (a, b) -> (a*c - b*s, b*c + a*s);
+// half split (llama.py:169-178): x*cos + rotate_half(x)*sin with rotate_half = (-hi, lo).
+__device__ __forceinline__ void rope_pair_interleaved(float a, float b, float c, float s, float& o0, float& o1) {
+    const float ac = a * c, bs = b * s, bc = b * c, as = a * s;
+    o0 = ac - bs;
+    o1 = bc + as;
+}
+__device__ __forceinline__ void rope_pair_half(float lo, float hi, float c_lo, float s_lo, float c_hi, float s_hi,
+                                               float& o_lo, float& o_hi) {
+    const float t0 = lo * c_lo, r0 = (-hi) * s_lo;
+    const float t1 = hi * c_hi, r1 = lo * s_hi;
+    o_lo = t0 + r0;
+    o_hi = t1 + r1;
+}
+
 }  // namespace smk

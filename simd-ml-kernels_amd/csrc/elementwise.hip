@@ -1,9 +1,16 @@
 // elementwise.hip -- SiLU, softmax rows, RMSNorm and RoPE for gfx950.
 //
-// SiLU follows silu_avx2.cpp:38-45: x / (1 + exp(-x)) with a correctly rounded division, and
-// the denominator forced to +inf when -x > 88 (so SiLU(-inf) is NaN and very negative x give
-// -0).  exp is ROCm's accurate expf (OCML, about 1 ulp), not a fast approximation: the
-// reference bounds SiLU at 1e-35 + 1e-6 |ref| (activations.hpp:20-23).
+// SiLU is bit-exact with the reference's SIMD tables (silu_avx2.cpp:38-45 with the exp of
+// simd_math.hpp:63-117): x / (1 + exp(-x)), IEEE division, the denominator forced to +inf
+// when -x > 88 (so SiLU(-inf) is NaN and very negative x give -0).
+//
+// Softmax rows follow softmax_row_avx2 (softmax_avx2.cpp:94-186): a NaN or +inf anywhere, or
+// every entry -inf, gives a NaN row; values of full groups of 8 get e = exp(x - max) by the
+// same exp, and their doubles go to eight running double sums (element i into sum i % 8, in
+// order), added as s0 + s1 + ... + s7; the last n % 8 values use a double exp of (x - max)
+// added in order after them; every output is then multiplied by float(1 / sum).  The double
+// exp of the tail is OCML's rather than glibc's: both are within one double ulp, so the
+// float results agree unless a double lands within an ulp of a float rounding boundary.
 //
 // RMSNorm and RoPE restate examples/llama/llama.py, where they are numpy code, and are
 // bit-exact with it:
@@ -24,46 +31,71 @@ namespace {
 
 __global__ void silu_kernel(const float* __restrict__ in, float* __restrict__ out, long long n) {
     for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n;
-         i += static_cast<long long>(gridDim.x) * blockDim.x) {
-        const float x = in[i];
-        const float nx = -x;
-        float d = 1.0f + expf(nx);
-        if (nx > 88.0f) d = __builtin_inff();
-        out[i] = x / d;
-    }
+         i += static_cast<long long>(gridDim.x) * blockDim.x)
+        out[i] = silu_ref(in[i]);
 }
 
-// One wave per row; FP64 exponentials and sum as the reference's scalar softmax
-// (scalar_kernels.cpp:200-222): a NaN or +inf anywhere, or every entry -inf, gives NaN.
-__global__ void softmax_kernel(const float* __restrict__ in, float* __restrict__ out, int rows, int n) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-    if (row >= rows) return;
+// One 256-thread workgroup per row, in softmax_row_avx2's order (see the top of this file).
+constexpr int kSoftmaxThreads = 256;
+
+__global__ __launch_bounds__(kSoftmaxThreads) void softmax_kernel(const float* __restrict__ in,
+                                                                  float* __restrict__ out, int rows, int n) {
+    __shared__ float red_f[kSoftmaxThreads / kWave];
+    __shared__ int red_i[kSoftmaxThreads / kWave];
+    __shared__ double lane_sum[8];
+    __shared__ float inv_s;
+    const int row = blockIdx.x;
     const float* x = in + static_cast<size_t>(row) * n;
     float* y = out + static_cast<size_t>(row) * n;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    constexpr int kWaves = kSoftmaxThreads / kWave;
     float mx = -__builtin_inff();
     int nonfinite = 0;
-    for (int i = lane; i < n; i += kWave) {
+    for (int i = threadIdx.x; i < n; i += kSoftmaxThreads) {
         const float v = x[i];
-        nonfinite |= (v != v) || (v == __builtin_inff());
+        const uint32_t u = __float_as_uint(v);
+        nonfinite |= (u & 0x7fffffffu) > 0x7f800000u || u == 0x7f800000u;
         mx = fmaxf(mx, v);
     }
     mx = group_max<kWave>(mx);
     nonfinite = group_sum_int<kWave>(nonfinite);
-    if (nonfinite || mx == -__builtin_inff()) {
-        for (int i = lane; i < n; i += kWave) y[i] = __builtin_nanf("");
+    if (lane == 0) {
+        red_f[wave] = mx;
+        red_i[wave] = nonfinite;
+    }
+    __syncthreads();
+    mx = red_f[0];
+    nonfinite = red_i[0];
+    for (int w = 1; w < kWaves; ++w) {
+        mx = fmaxf(mx, red_f[w]);
+        nonfinite |= red_i[w];
+    }
+    if (nonfinite || __float_as_uint(mx) == 0xff800000u) {
+        for (int i = threadIdx.x; i < n; i += kSoftmaxThreads) y[i] = __builtin_nanf("");
         return;
     }
-    double sum = 0.0;
-    for (int i = lane; i < n; i += kWave) {
-        const double e = exp(static_cast<double>(x[i]) - mx);
-        y[i] = static_cast<float>(e);
-        sum += e;
+    const int n8 = n - n % 8;
+    for (int i = threadIdx.x; i < n; i += kSoftmaxThreads) {
+        const float d = x[i] - mx;
+        y[i] = i < n8 ? exp_cody_waite(d) : static_cast<float>(exp(static_cast<double>(d)));
     }
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
-    const float inv = static_cast<float>(1.0 / sum);
-    for (int i = lane; i < n; i += kWave) y[i] = y[i] * inv;
+    __syncthreads();  // the e values are visible to the summing lanes
+    if (threadIdx.x < 8) {
+        double acc = 0.0;
+        for (int i = threadIdx.x; i < n8; i += 8) acc = acc + static_cast<double>(y[i]);
+        lane_sum[threadIdx.x] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = lane_sum[0];
+        for (int k = 1; k < 8; ++k) t = t + lane_sum[k];
+        double sum = 0.0 + t;
+        for (int i = n8; i < n; ++i) sum = sum + exp(static_cast<double>(x[i] - mx));
+        inv_s = static_cast<float>(1.0 / sum);
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    for (int i = threadIdx.x; i < n; i += kSoftmaxThreads) y[i] = y[i] * inv;
 }
 
 // numpy's float32 pairwise sum of q[0..n) (n <= 128 leaf: 8 interleaved accumulators).
@@ -287,17 +319,16 @@ __global__ void rope_kernel(const float* __restrict__ x, const float* __restrict
         float* yr = y + static_cast<size_t>(h) * hd;
         if (interleaved) {
             const float a = xr[2 * i], b = xr[2 * i + 1];
-            const float c = cs[i], s = sn[i];
-            const float ac = a * c, bs = b * s, bc = b * c, as = a * s;
-            yr[2 * i] = ac - bs;
-            yr[2 * i + 1] = bc + as;
+            float o0, o1;
+            rope_pair_interleaved(a, b, cs[i], sn[i], o0, o1);
+            yr[2 * i] = o0;
+            yr[2 * i + 1] = o1;
         } else {
-            // x*cos + rotate_half(x)*sin, rotate_half(x) = cat(-x[half:], x[:half]).
             const float lo = xr[i], hi = xr[half + i];
-            const float t0 = lo * cs[i], r0 = (-hi) * sn[i];
-            const float t1 = hi * cs[half + i], r1 = lo * sn[half + i];
-            yr[i] = t0 + r0;
-            yr[half + i] = t1 + r1;
+            float o0, o1;
+            rope_pair_half(lo, hi, cs[i], sn[i], cs[half + i], sn[half + i], o0, o1);
+            yr[i] = o0;
+            yr[half + i] = o1;
         }
     }
 }
@@ -316,8 +347,7 @@ hipError_t silu(const float* in, float* out, long long n, hipStream_t s) {
 
 hipError_t softmax_rows(const float* in, float* out, int rows, int n, hipStream_t s) {
     if (rows <= 0 || n <= 0) return hipSuccess;
-    const int per = 4;
-    hipLaunchKernelGGL(softmax_kernel, dim3((rows + per - 1) / per), dim3(per * kWave), 0, s, in, out, rows, n);
+    hipLaunchKernelGGL(softmax_kernel, dim3(rows), dim3(kSoftmaxThreads), 0, s, in, out, rows, n);
     return hipGetLastError();
 }
 

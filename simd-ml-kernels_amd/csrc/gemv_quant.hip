@@ -234,7 +234,7 @@ __device__ __forceinline__ float scale_b(const uint32_t (&w)[D]) { return half_b
 template <int BB, int LPR, int U, int MT, int NT>
 __global__ __launch_bounds__(NT) void gemv_pairs_kernel(int M, int N, int K, const float* __restrict__ x, int ldx,
                                                         const uint8_t* __restrict__ W, float* __restrict__ y, int ldy,
-                                                        int rows_per_wg) {
+                                                        int rows_per_wg, int accumulate) {
     using T = PairTraits<BB>;
     constexpr int D = T::kDwords;
     constexpr int G = kWave / LPR;                 // rows side by side in one wave
@@ -328,7 +328,10 @@ __global__ __launch_bounds__(NT) void gemv_pairs_kernel(int M, int N, int K, con
                     const float tot = group_sum<LPR>(acc[u][m]);
                     acc[u][m] = 0.0f;
                     const int r = rb + u * G;
-                    if (m < M && j == 0 && r < row_end) y[static_cast<size_t>(m) * ldy + r] = bad[m] ? __builtin_nanf("") : tot;
+                    if (m < M && j == 0 && r < row_end) {
+                        float* yp = y + static_cast<size_t>(m) * ldy + r;
+                        *yp = bad[m] ? __builtin_nanf("") : (accumulate ? *yp + tot : tot);
+                    }
                 }
             }
         }
@@ -342,12 +345,221 @@ __global__ __launch_bounds__(NT) void gemv_pairs_kernel(int M, int N, int K, con
     if (s < steps) body(s, wa, wb);
 }
 
+// ─── Q4_0 in the reference's SIMD order (y bit-exact with its AVX2 / AVX-512 tables) ─────
+// The reference's Q4_0 row loop (q4_0_rows.hpp:71-167, shared by its AVX2, AVX-VNNI and
+// AVX512-VNNI units) keeps four FP32 lanes per row: lane k holds the exact integer dot of the
+// block's values {4k..4k+3} and {16+4k..16+4k+3} (minus 8 times x's sum over them) and adds
+// fma(float(dot), fp16(d) * dx, acc) block after block; y = (acc0 + acc2) + (acc1 + acc3).
+// The last row of an odd N (q4_row_single) keeps eight lanes, the low-nibble and high-nibble
+// halves apart, and sums them lane-wise first.  Integer dots are exact in any order, so:
+//   phase 1 (parallel, as the pair kernel): a lane takes a 36-byte pair of one row and
+//     computes, for each block and each of the four reference lanes, the low-half and
+//     high-half integer dots (|dot| <= 4064: two int16 in one dword) and the block scale;
+//     they go to LDS, [row][block] with one padding entry per row (bank spread);
+//   phase 2: four lanes per row run the four FMA chains over the blocks in order, then DPP
+//     adds the lanes as the reference's horizontal sum does.
+__device__ __forceinline__ uint32_t pack_i16x2(int lo, int hi) {
+    return (static_cast<uint32_t>(lo) & 0xffffu) | (static_cast<uint32_t>(hi) << 16);
+}
+
+// Low and high integer dots of one reference lane: 4 quant bytes (nibble pairs) against x's
+// dword of values {4k..} (xl) and of values {16+4k..} (xh); -8 * sum(x) as the start.
+__device__ __forceinline__ uint32_t lane_dots(uint32_t q, uint32_t xl, uint32_t xh) {
+    constexpr uint32_t kMinus8 = 0xF8F8F8F8u;  // four int8 -8
+    const int dl = dot4(q & 0x0f0f0f0fu, xl, dot4(kMinus8, xl, 0));
+    const int dh = dot4((q >> 4) & 0x0f0f0f0fu, xh, dot4(kMinus8, xh, 0));
+    return pack_i16x2(dl, dh);
+}
+
+template <int LPR, int MT, int NT>
+__global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K, const float* __restrict__ x,
+                                                             int ldx, const uint8_t* __restrict__ W,
+                                                             float* __restrict__ y, int ldy, int rows_per_wg,
+                                                             int accumulate) {
+    constexpr int D = 9;
+    constexpr int G = kWave / LPR;           // rows side by side in one wave
+    constexpr int kWaves = NT / kWave;
+    constexpr int kRows = kWaves * G;        // rows of one group
+    constexpr int PQ = (MT * 1024 + NT - 1) / NT < 4 ? (MT * 1024 + NT - 1) / NT : 4;
+    static_assert(4 * kRows <= NT, "phase 2 needs four lanes per row");
+    extern __shared__ __align__(16) uint32_t lds[];
+    __shared__ int bad[MT];
+
+    const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
+    const int stride = nb + 1;
+    const size_t row_bytes = static_cast<size_t>(nb) * kQ4_0Bytes;
+    uint32_t* lds_q = lds;                                              // M * quads
+    float* lds_dx = reinterpret_cast<float*>(lds + M * quads);          // M * nb
+    const int x_words = (M * (quads + nb) + 3) & ~3;
+    uint4* part = reinterpret_cast<uint4*>(lds + x_words);              // M * kRows * stride
+    float* scl = reinterpret_cast<float*>(part + M * kRows * stride);   // M * kRows * stride
+
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int g = lane / LPR, j = lane % LPR;
+    const int rl = wave * G + g;             // this lane's row within the group (phase 1)
+    const int row0 = blockIdx.x * rows_per_wg;
+    const int row_end = min(N, row0 + rows_per_wg);
+    const int chunks = (pairs + LPR - 1) / LPR;
+    const int iters = (row_end - row0 + kRows - 1) / kRows;
+    const int steps = iters * chunks;
+
+    if (threadIdx.x < MT) bad[threadIdx.x] = 0;
+    lds_barrier();
+
+    auto load_step = [&](int s, uint32_t (&w)[D]) {
+        const int it = s / chunks, c = s - it * chunks;
+        const int p = min(j + c * LPR, pairs - 1);
+        const int r = min(row0 + it * kRows + rl, row_end - 1);
+        load_pair<D>(W + r * row_bytes + static_cast<size_t>(p) * (2 * kQ4_0Bytes), w);
+    };
+
+    XPreload<NT, PQ> xp;
+    xp.load(x, ldx, M, K);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t wa[D], wb[D];
+    load_step(0, wa);
+    __builtin_amdgcn_sched_barrier(0);
+    xp.template quantize<true, false>(x, ldx, M, K, lds_q, nullptr, lds_dx, bad);
+    lds_barrier();
+
+    auto phase2 = [&](int it) {
+        const int t = threadIdx.x;
+        if (t < 4 * kRows) {
+            const int r = t >> 2, k = t & 3;
+            const int row = row0 + it * kRows + r;
+            const bool single = (N & 1) && row == N - 1;
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (m >= M) break;
+                const uint32_t* pv = reinterpret_cast<const uint32_t*>(part + (m * kRows + r) * stride) + k;
+                const float* sv = scl + (m * kRows + r) * stride;
+                float a1 = 0.0f, a2 = 0.0f;
+                for (int b = 0; b < nb; ++b) {
+                    const uint32_t v = pv[4 * b];
+                    const float s = sv[b];
+                    const int dl = static_cast<int16_t>(v & 0xffffu), dh = static_cast<int>(v) >> 16;
+                    a1 = fmaf(static_cast<float>(single ? dl : dl + dh), s, a1);
+                    a2 = fmaf(static_cast<float>(dh), s, a2);
+                }
+                float tt = single ? a1 + a2 : a1;
+                tt = tt + dpp_f<kDppQuadXor2>(tt);   // lanes k and k + 2
+                tt = tt + dpp_f<kDppQuadXor1>(tt);   // then the two pair sums
+                if (k == 0 && row < row_end) {
+                    float* yp = y + static_cast<size_t>(m) * ldy + row;
+                    *yp = bad[m] ? __builtin_nanf("") : (accumulate ? *yp + tt : tt);
+                }
+            }
+        }
+    };
+
+    auto body = [&](int s, uint32_t (&cur)[D], uint32_t (&nxt)[D]) {
+        load_step(s + 1 < steps ? s + 1 : s, nxt);
+        const int it = s / chunks, c = s - it * chunks;
+        const int p = j + c * LPR;
+        if (p < pairs) {
+            uint32_t qa[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) qa[k] = skip2(cur[k + 1], cur[k]);
+            const float hA = half_bits_to_float(cur[0]), hB = half_bits_to_float(cur[4] >> 16);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (m < M) {
+                    const uint4* planes = reinterpret_cast<const uint4*>(lds_q + m * quads);
+                    const uint4 x0 = planes[p], x1 = planes[pairs + p], x2 = planes[2 * pairs + p],
+                                x3 = planes[3 * pairs + p];
+                    uint4 pa, pb;
+                    pa.x = lane_dots(qa[0], x0.x, x1.x);
+                    pa.y = lane_dots(qa[1], x0.y, x1.y);
+                    pa.z = lane_dots(qa[2], x0.z, x1.z);
+                    pa.w = lane_dots(qa[3], x0.w, x1.w);
+                    pb.x = lane_dots(cur[5], x2.x, x3.x);
+                    pb.y = lane_dots(cur[6], x2.y, x3.y);
+                    pb.z = lane_dots(cur[7], x2.z, x3.z);
+                    pb.w = lane_dots(cur[8], x2.w, x3.w);
+                    const int e = (m * kRows + rl) * stride + 2 * p;
+                    part[e] = pa;
+                    part[e + 1] = pb;
+                    scl[e] = hA * lds_dx[m * nb + 2 * p];
+                    scl[e + 1] = hB * lds_dx[m * nb + 2 * p + 1];
+                }
+            }
+        }
+        if (c == chunks - 1) {
+            lds_barrier();  // the group's partials are in LDS
+            phase2(it);
+            lds_barrier();  // read before the next group overwrites them
+        }
+    };
+
+    int s = 0;
+    for (; s + 1 < steps; s += 2) {
+        body(s, wa, wb);
+        body(s + 1, wb, wa);
+    }
+    if (s < steps) body(s, wa, wb);
+}
+
+// Odd K/32 or a 2-byte aligned W: four lanes per row walk the blocks themselves (16-bit
+// loads), in the same order; 64 rows per 256-thread workgroup.
+template <int MT>
+__global__ __launch_bounds__(kThreads) void gemv_q4_ordered_generic_kernel(int M, int N, int K,
+                                                                           const float* __restrict__ x, int ldx,
+                                                                           const uint8_t* __restrict__ W,
+                                                                           float* __restrict__ y, int ldy,
+                                                                           int accumulate) {
+    extern __shared__ __align__(16) uint32_t lds[];
+    __shared__ int bad[MT];
+    const int nb = K >> 5, quads = K >> 2;
+    uint32_t* lds_q = lds;
+    float* lds_dx = reinterpret_cast<float*>(lds + M * quads);
+    if (threadIdx.x < MT) bad[threadIdx.x] = 0;
+    lds_barrier();
+    quantize_x_into_lds<false, false>(x, ldx, M, K, lds_q, nullptr, lds_dx, bad);
+    lds_barrier();
+    const int r = threadIdx.x >> 2, k = threadIdx.x & 3;
+    const int row = blockIdx.x * (kThreads / 4) + r;
+    const int rr = min(row, N - 1);
+    const bool single = (N & 1) && row == N - 1;
+    float a1[MT], a2[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) a1[m] = a2[m] = 0.0f;
+    const uint8_t* wrow = W + static_cast<size_t>(rr) * nb * kQ4_0Bytes;
+    for (int b = 0; b < nb; ++b) {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(wrow + static_cast<size_t>(b) * kQ4_0Bytes);
+        const uint32_t q = static_cast<uint32_t>(h[1 + 2 * k]) | (static_cast<uint32_t>(h[2 + 2 * k]) << 16);
+        const float hd = half_bits_to_float(h[0]);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m >= M) break;
+            const uint32_t* xb = lds_q + m * quads + 8 * b;
+            const uint32_t v = lane_dots(q, xb[k], xb[4 + k]);
+            const int dl = static_cast<int16_t>(v & 0xffffu), dh = static_cast<int>(v) >> 16;
+            const float s = hd * lds_dx[m * nb + b];
+            a1[m] = fmaf(static_cast<float>(single ? dl : dl + dh), s, a1[m]);
+            a2[m] = fmaf(static_cast<float>(dh), s, a2[m]);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (m >= M) break;
+        float tt = single ? a1[m] + a2[m] : a1[m];
+        tt = tt + dpp_f<kDppQuadXor2>(tt);
+        tt = tt + dpp_f<kDppQuadXor1>(tt);
+        if (k == 0 && row < N) {
+            float* yp = y + static_cast<size_t>(m) * ldy + row;
+            *yp = bad[m] ? __builtin_nanf("") : (accumulate ? *yp + tt : tt);
+        }
+    }
+}
+
 // ─── the generic kernel (any K/32, W 2-byte aligned) ─────────────────────────
 // One wave per row, lanes over blocks; 16-bit loads.  Used for odd K/32 only.
 template <int BB, int MT>
 __global__ __launch_bounds__(kThreads) void gemv_generic_kernel(int M, int N, int K, const float* __restrict__ x,
                                                                 int ldx, const uint8_t* __restrict__ W,
-                                                                float* __restrict__ y, int ldy, int rows_per_wg) {
+                                                                float* __restrict__ y, int ldy, int rows_per_wg,
+                                                                int accumulate) {
     constexpr bool kQ4 = BB == kQ4_0Bytes;
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ int bad[MT];
@@ -395,7 +607,10 @@ __global__ __launch_bounds__(kThreads) void gemv_generic_kernel(int M, int N, in
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             const float tot = group_sum<kWave>(acc[m]);
-            if (m < M && lane == 0) y[static_cast<size_t>(m) * ldy + r] = bad[m] ? __builtin_nanf("") : tot;
+            if (m < M && lane == 0) {
+                float* yp = y + static_cast<size_t>(m) * ldy + r;
+                *yp = bad[m] ? __builtin_nanf("") : (accumulate ? *yp + tot : tot);
+            }
         }
     }
 }
@@ -470,7 +685,7 @@ int choose_lpr(int pairs) {
 
 template <int BB, int LPR, int U, int MT, int NT>
 hipError_t launch_pairs(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
-                        int rows_per_wg, hipStream_t stream) {
+                        int rows_per_wg, int acc, hipStream_t stream) {
     constexpr int G = kWave / LPR;
     constexpr int kRowsPerIter = (NT / kWave) * G * U;
     if (rows_per_wg <= 0) {
@@ -483,27 +698,27 @@ hipError_t launch_pairs(int M, int N, int K, const float* x, int ldx, const uint
     const int grid = (N + rows_per_wg - 1) / rows_per_wg;
     if (const hipError_t e = allow_lds(gemv_pairs_kernel<BB, LPR, U, MT, NT>, lds); e != hipSuccess) return e;
     hipLaunchKernelGGL((gemv_pairs_kernel<BB, LPR, U, MT, NT>), dim3(grid), dim3(NT), lds, stream, M, N, K, x, ldx, W,
-                       y, ldy, rows_per_wg);
+                       y, ldy, rows_per_wg, acc);
     return hipGetLastError();
 }
 
 template <int BB, int U, int MT, int NT>
 hipError_t launch_pairs_lpr(int lpr, int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y,
-                            int ldy, int rows_per_wg, hipStream_t stream) {
+                            int ldy, int rows_per_wg, int acc, hipStream_t stream) {
     switch (lpr) {
-        case 64: return launch_pairs<BB, 64, U, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
-        case 32: return launch_pairs<BB, 32, U, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
-        case 16: return launch_pairs<BB, 16, U, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
-        default: return launch_pairs<BB, 8, U, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, stream);
+        case 64: return launch_pairs<BB, 64, U, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, stream);
+        case 32: return launch_pairs<BB, 32, U, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, stream);
+        case 16: return launch_pairs<BB, 16, U, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, stream);
+        default: return launch_pairs<BB, 8, U, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, stream);
     }
 }
 
 // One row of x: workgroup size and unroll are tunable.
 template <int BB>
 hipError_t launch_pairs_m1(int lpr, int nt, int u, int N, int K, const float* x, int ldx, const uint8_t* W, float* y,
-                           int ldy, int rpw, hipStream_t s) {
+                           int ldy, int rpw, int acc, hipStream_t s) {
 #define SMK_PAIRS_M1(NT_, U_) \
-    if (nt == NT_ && u == U_) return launch_pairs_lpr<BB, U_, 1, NT_>(lpr, 1, N, K, x, ldx, W, y, ldy, rpw, s);
+    if (nt == NT_ && u == U_) return launch_pairs_lpr<BB, U_, 1, NT_>(lpr, 1, N, K, x, ldx, W, y, ldy, rpw, acc, s);
     SMK_PAIRS_M1(256, 1) SMK_PAIRS_M1(256, 2) SMK_PAIRS_M1(256, 4)
     SMK_PAIRS_M1(512, 1) SMK_PAIRS_M1(512, 2) SMK_PAIRS_M1(512, 4)
     SMK_PAIRS_M1(1024, 1) SMK_PAIRS_M1(1024, 2) SMK_PAIRS_M1(1024, 4)
@@ -513,27 +728,117 @@ hipError_t launch_pairs_m1(int lpr, int nt, int u, int N, int K, const float* x,
 
 template <int BB, int MT>
 hipError_t launch_generic(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
-                          hipStream_t stream) {
+                          int acc, hipStream_t stream) {
     const int rows_per_wg = 16;
     const int nb = K >> 5;
     const size_t lds = static_cast<size_t>(M) * (K + 8 * nb);
     const int grid = (N + rows_per_wg - 1) / rows_per_wg;
     if (const hipError_t e = allow_lds(gemv_generic_kernel<BB, MT>, lds); e != hipSuccess) return e;
     hipLaunchKernelGGL((gemv_generic_kernel<BB, MT>), dim3(grid), dim3(kThreads), lds, stream, M, N, K, x, ldx, W, y,
-                       ldy, rows_per_wg);
+                       ldy, rows_per_wg, acc);
     return hipGetLastError();
+}
+
+// ─── Q4_0 launchers (the reference's SIMD order) ─────────────────────────────
+
+size_t ordered_lds_bytes(int M, int K, int rows_per_group) {
+    const size_t nb = static_cast<size_t>(K) >> 5, quads = static_cast<size_t>(K) >> 2;
+    const size_t x_words = (M * (quads + nb) + 3) & ~static_cast<size_t>(3);
+    return 4 * x_words + static_cast<size_t>(M) * rows_per_group * (nb + 1) * 20;
+}
+
+template <int LPR, int MT, int NT>
+hipError_t launch_ordered(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
+                          int rows_per_wg, int acc, hipStream_t stream) {
+    constexpr int kRows = NT / LPR;
+    const size_t lds = ordered_lds_bytes(M, K, kRows);
+    if (rows_per_wg <= 0) rows_per_wg = std::max(kRows, (N + 511) / 512);
+    const int grid = (N + rows_per_wg - 1) / rows_per_wg;
+    if (const hipError_t e = allow_lds(gemv_q4_ordered_kernel<LPR, MT, NT>, lds); e != hipSuccess) return e;
+    hipLaunchKernelGGL((gemv_q4_ordered_kernel<LPR, MT, NT>), dim3(grid), dim3(NT), lds, stream, M, N, K, x, ldx, W, y,
+                       ldy, rows_per_wg, acc);
+    return hipGetLastError();
+}
+
+template <int MT, int NT>
+hipError_t launch_ordered_lpr(int lpr, int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y,
+                              int ldy, int rows_per_wg, int acc, hipStream_t s) {
+    switch (lpr) {
+        case 64: return launch_ordered<64, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, s);
+        case 32: return launch_ordered<32, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, s);
+        case 16: return launch_ordered<16, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, s);
+        default: return launch_ordered<8, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, s);
+    }
+}
+
+template <int MT>
+hipError_t launch_ordered_generic(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
+                                  int acc, hipStream_t stream) {
+    const size_t lds = static_cast<size_t>(M) * ((K >> 2) + (K >> 5)) * 4;
+    const int grid = (N + kThreads / 4 - 1) / (kThreads / 4);
+    if (const hipError_t e = allow_lds(gemv_q4_ordered_generic_kernel<MT>, lds); e != hipSuccess) return e;
+    hipLaunchKernelGGL(gemv_q4_ordered_generic_kernel<MT>, dim3(grid), dim3(kThreads), lds, stream, M, N, K, x, ldx,
+                       W, y, ldy, acc);
+    return hipGetLastError();
+}
+
+hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
+                           hipStream_t stream, const GemvTuning* t) {
+    const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+    const int acc = t ? t->accumulate : 0;
+    const int pairs = (K >> 5) / 2;
+    constexpr size_t kLdsCap = 150 * 1024;
+    const bool generic = !pair_path_ok(K, W) || ordered_lds_bytes(M, K, 256 / 64) > kLdsCap;
+    if (generic) {
+        switch (mt) {
+            case 1: return launch_ordered_generic<1>(M, N, K, x, ldx, W, y, ldy, acc, stream);
+            case 2: return launch_ordered_generic<2>(M, N, K, x, ldx, W, y, ldy, acc, stream);
+            case 4: return launch_ordered_generic<4>(M, N, K, x, ldx, W, y, ldy, acc, stream);
+            default: return launch_ordered_generic<8>(M, N, K, x, ldx, W, y, ldy, acc, stream);
+        }
+    }
+    // The lane split does not change the result here (every row's sum has the reference's
+    // order), so it is chosen for speed only.
+    int lpr = (t && t->lanes_per_row) ? t->lanes_per_row : (pairs >= 128 ? 64 : pairs >= 32 ? 32 : pairs >= 16 ? 16 : 8);
+    int rpw = t ? t->rows_per_wg : 0;
+    if (mt == 1) {
+        const double bytes = static_cast<double>(N) * (K >> 5) * kQ4_0Bytes;
+        const int per_cu = bytes < 24e6 ? 1 : (bytes < 128e6 ? 2 : 4);
+        if (rpw <= 0) rpw = std::max(1, (N + g_cus * per_cu - 1) / (g_cus * per_cu));
+        int nt = (t && t->threads) ? t->threads : ((bytes < 24e6 || bytes >= 128e6) ? 1024 : 512);
+        if (!(t && t->threads)) {
+            while (nt > 256 && nt > rpw * lpr) nt /= 2;
+            while (nt > 256 && ordered_lds_bytes(1, K, nt / lpr) > kLdsCap) nt /= 2;
+        }
+        while (ordered_lds_bytes(1, K, nt / lpr) > kLdsCap && lpr < 64) lpr *= 2;
+        switch (nt) {
+            case 1024: return launch_ordered_lpr<1, 1024>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
+            case 512: return launch_ordered_lpr<1, 512>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
+            default: return launch_ordered_lpr<1, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
+        }
+    }
+    lpr = ordered_lds_bytes(M, K, 256 / 32) <= kLdsCap && lpr <= 32 ? 32 : 64;
+    switch (mt) {
+        case 2: return launch_ordered_lpr<2, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
+        case 4: return launch_ordered_lpr<4, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
+        default: return launch_ordered_lpr<8, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
+    }
 }
 
 template <int BB>
 hipError_t gemv_quant_fmt(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
                           hipStream_t stream, const GemvTuning* t) {
+    if constexpr (BB == kQ4_0Bytes) {
+        if (!(t && t->unordered)) return gemv_q4_ordered(M, N, K, x, ldx, W, y, ldy, stream, t);
+    }
     const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+    const int acc = t ? t->accumulate : 0;
     if (!pair_path_ok(K, W)) {
         switch (mt) {
-            case 1: return launch_generic<BB, 1>(M, N, K, x, ldx, W, y, ldy, stream);
-            case 2: return launch_generic<BB, 2>(M, N, K, x, ldx, W, y, ldy, stream);
-            case 4: return launch_generic<BB, 4>(M, N, K, x, ldx, W, y, ldy, stream);
-            default: return launch_generic<BB, 8>(M, N, K, x, ldx, W, y, ldy, stream);
+            case 1: return launch_generic<BB, 1>(M, N, K, x, ldx, W, y, ldy, acc, stream);
+            case 2: return launch_generic<BB, 2>(M, N, K, x, ldx, W, y, ldy, acc, stream);
+            case 4: return launch_generic<BB, 4>(M, N, K, x, ldx, W, y, ldy, acc, stream);
+            default: return launch_generic<BB, 8>(M, N, K, x, ldx, W, y, ldy, acc, stream);
         }
     }
     // The lane split fixes the summation order, so it depends on K only: every row of a
@@ -556,13 +861,13 @@ hipError_t gemv_quant_fmt(int M, int N, int K, const float* x, int ldx, const ui
         if (!(t && t->threads))
             while (nt > 256 && nt > rpw * lpr) nt /= 2;
         const int u = (t && t->unroll) ? t->unroll : 1;
-        return launch_pairs_m1<BB>(lpr, nt, u, N, K, x, ldx, W, y, ldy, rpw, stream);
+        return launch_pairs_m1<BB>(lpr, nt, u, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
     }
     constexpr int U2 = BB == kQ4_0Bytes ? 4 : 2, U4 = BB == kQ4_0Bytes ? 2 : 1;
     switch (mt) {
-        case 2: return launch_pairs_lpr<BB, U2, 2, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
-        case 4: return launch_pairs_lpr<BB, U4, 4, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
-        default: return launch_pairs_lpr<BB, U4, 8, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, stream);
+        case 2: return launch_pairs_lpr<BB, U2, 2, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
+        case 4: return launch_pairs_lpr<BB, U4, 4, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
+        default: return launch_pairs_lpr<BB, U4, 8, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
     }
 }
 
@@ -580,6 +885,7 @@ hipError_t gemv_quant(int block_bytes, int M, int N, int K, const float* x, int 
     if (N <= 0 || M <= 0) return hipSuccess;
     if (M > 8 || K < 0 || K % 32 != 0) return hipErrorInvalidValue;
     if (K == 0) {
+        if (tuning && tuning->accumulate) return hipSuccess;  // y + 0
         for (int m = 0; m < M; ++m) {
             const hipError_t e = fill(y + static_cast<size_t>(m) * ldy, N, 0.0f, stream);
             if (e != hipSuccess) return e;

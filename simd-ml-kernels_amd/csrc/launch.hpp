@@ -12,12 +12,15 @@ namespace smk {
 constexpr int kQ4_0Bytes = 18;
 constexpr int kQ8_0Bytes = 34;
 
-// Tuning knobs of the quantized GEMV; zero fields take the built-in choice.
+// Options of the quantized GEMV; zero fields take the built-in choice.
 struct GemvTuning {
     int lanes_per_row = 0;  // 8, 16, 32 or 64 lanes share one row of W
     int rows_per_wg = 0;    // rows of W per workgroup
     int threads = 0;        // threads per workgroup: 256, 512 or 1024 (one row of x only)
     int unroll = 0;         // rows per lane group per step: 1, 2 or 4 (one row of x only)
+    int accumulate = 0;     // 1: y = y + x.W^T (one float32 add per output: a residual update)
+    int unordered = 0;      // Q4_0 only, diagnostics: the free-order pair kernel instead of the
+                            // reference's SIMD summation order
 };
 
 // y[m*ldy + n] = sum_k x[m*ldx + k] * W[n][k] for m < M (M <= 8), W in GGUF Q4_0 (block_bytes 18)

@@ -7,6 +7,7 @@
 // stream and scratch, created on its first call; the weight cache is shared and guarded by a
 // mutex.  A device copy in the cache is never freed while a call may read it: unpinning or
 // eviction first synchronizes the device.
+#include "abi_internal.hpp"
 #include "launch.hpp"
 #include "smk_hip.h"
 
@@ -21,9 +22,13 @@
 #include <mutex>
 #include <string>
 
-namespace {
+namespace smk::abi {
 
+namespace {
 thread_local std::string t_error;
+}  // namespace
+
+const char* last_error() { return t_error.c_str(); }
 
 int ok() {
     t_error.clear();
@@ -39,12 +44,6 @@ int hip_fail(hipError_t e, const char* what) {
     const int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? SMK_ERR_OUT_OF_MEMORY : SMK_ERR_DEVICE;
     return fail(code, std::string(what) + ": " + hipGetErrorString(e));
 }
-
-#define SMK_HIP(call, what)                          \
-    do {                                             \
-        const hipError_t e_ = (call);                \
-        if (e_ != hipSuccess) return hip_fail(e_, what); \
-    } while (0)
 
 // ─── device ─────────────────────────────────────────────────────────────────
 
@@ -100,6 +99,12 @@ int use_device() {
     if (hipGetDevice(&cur) != hipSuccess || cur != d.id) SMK_HIP(hipSetDevice(d.id), "hipSetDevice");
     return SMK_OK;
 }
+
+}  // namespace smk::abi
+
+namespace {
+
+using namespace smk::abi;
 
 // ─── per-thread context ─────────────────────────────────────────────────────
 
@@ -322,7 +327,7 @@ int host_gemm(int elem, bool ta, bool tb, int M, int N, int K, float alpha, cons
 
 extern "C" {
 
-const char* smk_last_error(void) { return t_error.c_str(); }
+const char* smk_last_error(void) { return smk::abi::last_error(); }
 
 const char* smk_version(void) { return "simd-ml-kernels-amd 0.1.0 (gfx950)"; }
 
@@ -692,6 +697,12 @@ int smk_runtime_version(int* runtime, int* built) {
         *runtime = 0;
         SMK_HIP(hipRuntimeGetVersion(runtime), "hipRuntimeGetVersion");
     }
+    return ok();
+}
+
+int smk_set_q4_order(int reference_order) {
+    if (reference_order != 0 && reference_order != 1) return fail(SMK_ERR_ARGUMENT, "reference_order must be 0 or 1");
+    g_tuning.unordered = reference_order ? 0 : 1;
     return ok();
 }
 

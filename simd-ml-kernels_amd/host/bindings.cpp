@@ -74,7 +74,10 @@ py::array_t<float> output_matrix(const py::object& C, py::ssize_t M, py::ssize_t
 // ─── residency of read-only weights ──────────────────────────────────────────
 
 std::mutex g_pin_mu;
-std::map<const void*, py::object> g_pinned;  // data pointer -> the array (kept alive)
+// data pointer -> the array (kept alive).  Allocated once and never destroyed by C++: its
+// references are dropped by an atexit hook while the interpreter still runs (a static map's
+// destructor would run after Python has finalized and decrement without the GIL).
+std::map<const void*, py::object>& g_pinned = *new std::map<const void*, py::object>();
 
 size_t pin_budget() {
     static const size_t b = [] {
@@ -437,6 +440,16 @@ PYBIND11_MODULE(_core, m) {
         "simd-ml-kernels on AMD Instinct MI355X (gfx950): decode GEMV (Q4_0, Q8_0, FP16, BF16, FP32),\n"
         "SiLU, softmax, RMSNorm and RoPE on NumPy arrays, computed by hand-written HIP kernels.\n"
         "Arrays are never converted; read-only weight arrays stay resident in HBM after first use.";
+
+    // Drop the resident arrays (and their device copies) at interpreter exit, with the GIL held.
+    py::module_::import("atexit").attr("register")(py::cpp_function([]() {
+        std::map<const void*, py::object> drop;
+        {
+            std::lock_guard<std::mutex> lk(g_pin_mu);
+            drop.swap(g_pinned);
+        }
+        for (auto& kv : drop) smk_weights_unpin(kv.first);
+    }));
 
     auto dtype_error = py::register_exception<DTypeError>(
         m, "DTypeError", py::make_tuple(py::handle(PyExc_TypeError), py::handle(PyExc_RuntimeError)));

@@ -24,6 +24,17 @@ SMK_ERR_DATA = 5
 
 _i, _ll, _f, _p, _sz = ctypes.c_int, ctypes.c_longlong, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
 
+class LlamaConfig(ctypes.Structure):
+    """smk_llama_config of include/smk_hip.h."""
+    _fields_ = [(n, ctypes.c_int) for n in ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim", "ffn", "vocab",
+                                            "matrix_type", "embed_type", "head_type", "rope_interleaved")] + \
+               [("rms_eps", ctypes.c_double)]
+
+
+# Tensor ids of smk_llama_set_tensor.
+LLAMA_TENSORS = {"token_embd": 0, "output_norm": 1, "output": 2, "attn_norm": 3, "attn_q": 4, "attn_k": 5,
+                 "attn_v": 6, "attn_output": 7, "ffn_norm": 8, "ffn_gate": 9, "ffn_up": 10, "ffn_down": 11}
+
 # name -> argument types (all return int unless listed in _RESTYPE)
 SIGNATURES = {
     "smk_last_error": [],
@@ -60,6 +71,13 @@ SIGNATURES = {
     "smk_d_block_sums": [_i, _i, _i, _p, _p, _p, _p],
     "smk_d_read_roof": [_p, _sz, _p, _i, _p],
     "smk_d_copy": [_p, _p, _sz, _p],
+    "smk_llama_create": [_p, ctypes.POINTER(_p)],
+    "smk_llama_destroy": [_p],
+    "smk_llama_set_tensor": [_p, _i, _i, _p, _sz],
+    "smk_llama_reset": [_p, _i, _p, _p],
+    "smk_llama_step": [_p, _i, _p],
+    "smk_llama_generate": [_p, _p, _i, _i, _p, _p],
+    "smk_llama_info": [_p, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(ctypes.c_ulonglong)],
     "smk_malloc": [ctypes.POINTER(_p), _sz],
     "smk_free": [_p],
     "smk_memcpy_h2d": [_p, _p, _sz],
@@ -80,6 +98,7 @@ SIGNATURES = {
     "smk_graph_destroy": [_p],
     "smk_runtime_version": [ctypes.POINTER(_i), ctypes.POINTER(_i)],
     "smk_set_gemv_tuning": [_i, _i, _i, _i],
+    "smk_set_q4_order": [_i],
     "smk_gemv_path": [_i, _p],
 }
 _RESTYPE = {"smk_last_error": ctypes.c_char_p, "smk_version": ctypes.c_char_p, "smk_gemv_path": ctypes.c_char_p}

@@ -1,0 +1,138 @@
+"""GPU parity of the Llama decode loop against the reference's CPU loop.
+
+* Tiny models: the device engine's greedy tokens equal the reference loop's
+  (oracle/llama_ref.py with the reference's own kernels when oracle/_ref is built, else the
+  oracle's restatement of their order).  With Q4_0 matrices every logit is bit-identical at
+  every step (GEMV, attention, softmax and SiLU follow the reference's SIMD order; RMSNorm and
+  RoPE its numpy code); with Q8_0 / F32 matrices the logits stay within 2e-4.  The
+  module-call loop (device_loop=False) gives the same tokens and logits within 2e-4.
+* Llama-3.2-1B shape, seed 5, Q4_0: 32-token prompt and 128 greedy tokens equal the committed
+  tokens of the reference's CPU loop (tests/golden/make_llama_tokens.py).
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import llama_ref as lr
+from oracle import oracle as o
+from simd_ml_kernels import gguf, llama
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+TINY = {"model_type": "llama", "hidden_size": 256, "intermediate_size": 512, "num_hidden_layers": 2,
+        "num_attention_heads": 4, "num_key_value_heads": 2, "head_dim": 64, "vocab_size": 1000,
+        "rms_norm_eps": 1e-5, "rope_theta": 500000.0, "tie_word_embeddings": True,
+        "rope_scaling": {"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                         "original_max_position_embeddings": 8192}}
+WTYPES = {"q4_0": (gguf.Q4_0, lr.Q4_0), "q8_0": (gguf.Q8_0, lr.Q8_0), "f32": (gguf.F32, lr.F32)}
+
+
+def _oracle_kind():
+    return "reference" if o.ref() is not None and o.ref_best_isa() in ("avx2", "avx512") else "simd"
+
+
+def _tiny(tmp_path, wname, seed=21, n_prompt=8):
+    gtype, ltype = WTYPES[wname]
+    path, prompt = llama.write_synthetic_model(str(tmp_path), TINY, seed=seed, n_prompt=n_prompt, weight_type=gtype)
+    c = lr.Cfg.from_config(TINY)
+    oprompt, W = lr.synthetic_model(c, seed, n_prompt, ltype)
+    assert prompt == oprompt
+    return path, prompt, lr.Decoder(c, W, ltype, _oracle_kind())
+
+
+@pytest.mark.parametrize("wname", ["q4_0", "q8_0", "f32"])
+def test_tiny_engine_matches_reference_loop(tmp_path, wname):
+    path, prompt, dec = _tiny(tmp_path, wname)
+    ids_ref, margins, _ = dec.generate(prompt, 16)
+    m = llama.Llama(str(tmp_path), gguf=path)
+    try:
+        ids = list(m.generate(prompt, 16, stop_at_eos=False))
+        assert ids == ids_ref, (ids, ids_ref, margins)
+        # Teacher-forced: logits of every position against the reference loop.
+        seq = prompt + ids_ref[:-1]
+        m.reset(len(seq))
+        dec.reset(len(seq))
+        for i, t in enumerate(seq):
+            lg = m.step(t)
+            lo = dec.step(t)
+            if wname == "q4_0":
+                np.testing.assert_array_equal(lg.view(np.uint32), lo.view(np.uint32), err_msg=f"position {i}")
+            else:
+                assert np.abs(lg - lo).max() <= 2e-4, np.abs(lg - lo).max()
+            assert int(np.argmax(lg)) == int(np.argmax(lo))
+    finally:
+        m.close()
+
+
+def test_tiny_module_loop_matches_engine(tmp_path):
+    path, prompt, _ = _tiny(tmp_path, "q4_0", seed=22)
+    eng = llama.Llama(str(tmp_path), gguf=path)
+    host = llama.Llama(str(tmp_path), gguf=path, device_loop=False)
+    try:
+        seq = prompt + [5, 17, 999, 0]
+        eng.reset(len(seq))
+        host.reset(len(seq))
+        for t in seq:
+            a, b = eng.step(t), host.step(t)
+            assert np.abs(a - b).max() <= 2e-4
+        assert list(eng.generate(prompt, 10, stop_at_eos=False)) == list(host.generate(prompt, 10, stop_at_eos=False))
+        # logits=False skips the lm_head and still advances the position.
+        eng.reset(4)
+        assert eng.step(prompt[0], logits=False) is None and eng.pos == 1
+    finally:
+        eng.close()
+        host.close()
+
+
+def test_tiny_generate_stops_at_eos_and_reports_stats(tmp_path):
+    path, prompt, dec = _tiny(tmp_path, "q4_0", seed=23)
+    ids_ref, _, _ = dec.generate(prompt, 12)
+    m = llama.Llama(str(tmp_path), gguf=path)
+    try:
+        m.cfg.eos_token_ids = (ids_ref[3],)
+        stats = {}
+        ids = list(m.generate(prompt, 12, stats=stats))
+        assert ids == ids_ref[:ids_ref.index(ids_ref[3]) + 1]
+        assert stats["prefill_tokens"] == len(prompt) and stats["decode_steps"] == 11 and stats["decode_s"] > 0
+    finally:
+        m.close()
+
+
+def test_engine_rejects_bad_calls(tmp_path):
+    path, prompt, _ = _tiny(tmp_path, "q4_0", seed=24)
+    m = llama.Llama(str(tmp_path), gguf=path)
+    try:
+        with pytest.raises(RuntimeError):
+            m.step(0)  # no reset yet
+        m.reset(2)
+        with pytest.raises(RuntimeError):
+            m._engine.step(1000, True)  # token out of range (vocab 1000)
+        m.step(1)
+        m.step(2)
+        with pytest.raises(ValueError):
+            m.step(3)  # cache full
+    finally:
+        m.close()
+
+
+def test_llama_3_2_1b_greedy_tokens_equal_reference(tmp_path):
+    """32-token prompt, 128 greedy tokens, token-identical with the
+    reference's CPU loop on the same seeded model."""
+    with open(os.path.join(HERE, "golden", "llama_3_2_1b_q4_0_seed5.json")) as f:
+        gold = json.load(f)
+    print(f"writing the synthetic Llama-3.2-1B (seed {gold['seed']})", flush=True)
+    path, prompt = llama.write_synthetic_model(str(tmp_path), gold["config"], seed=gold["seed"],
+                                               n_prompt=len(gold["prompt"]))
+    assert prompt == gold["prompt"]
+    m = llama.Llama(str(tmp_path), gguf=path)
+    try:
+        stats = {}
+        ids = list(m.generate(prompt, gold["n_new"], stats=stats, stop_at_eos=False))
+        print(f"decode {stats['decode_steps'] / stats['decode_s']:.1f} tok/s", flush=True)
+        assert ids == gold["tokens"]
+    finally:
+        m.close()

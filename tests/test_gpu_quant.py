@@ -179,6 +179,53 @@ class TestGemv:
         assert (np.abs(y - ref) <= o.gemv_bound(K, mag)).all()
 
 
+class TestQ4ReferenceOrder:
+    """Q4_0 y is bit-exact with the reference's SIMD tables (q4_0_rows.hpp: four FMA chains per
+    row, the odd last row in eight), restated in oracle/smk_oracle.c and pinned there to the
+    reference's own AVX-512 build; against oracle/_ref directly where it is present."""
+
+    SHAPES = [(1, 64), (2, 64), (3, 64), (7, 96), (8, 2048), (9, 2048), (77, 4096), (33, 11008), (300, 2048),
+              (1001, 2048), (5, 8192), (3072, 2048), (2048, 8192), (4, 14336)]
+
+    @pytest.mark.parametrize("N,K", SHAPES)
+    def test_bit_exact_with_reference_order(self, N, K):
+        x, wq = _inputs("q4_0", N, K, N * 31 + K)
+        y = d_gemv("q4_0", x, wq, N, K)
+        np.testing.assert_array_equal(y.view(np.uint32), o.gemv_q4_0_simd(x, wq, N, K).view(np.uint32))
+        R = o.ref()
+        if R is not None and o.ref_best_isa() in ("avx2", "avx512"):
+            yr = np.empty(N, np.float32)
+            R.ref_gemv_q4_0(o.ISA[o.ref_best_isa()], N, K, x.ctypes.data_as(o._f32p), wq.ctypes.data_as(o._u8p),
+                            yr.ctypes.data_as(o._f32p))
+            np.testing.assert_array_equal(y.view(np.uint32), yr.view(np.uint32))
+
+    @pytest.mark.parametrize("N,K", [(13, 2048), (12, 96), (5, 32)])
+    def test_generic_path_same_order(self, N, K):
+        """Odd K/32 and a 2-byte aligned W take the generic kernel: same bits."""
+        x, wq = _inputs("q4_0", N, K, 99)
+        ref = o.gemv_q4_0_simd(x, wq, N, K)
+        for off in (0, 2):
+            y = d_gemv("q4_0", x, wq, N, K, offset=off)
+            np.testing.assert_array_equal(y.view(np.uint32), ref.view(np.uint32))
+
+    @pytest.mark.parametrize("lpr", [8, 16, 32, 64])
+    def test_lane_split_does_not_change_bits(self, lpr):
+        N, K = 131, 4096
+        x, wq = _inputs("q4_0", N, K, 5)
+        g.call("smk_set_gemv_tuning", lpr, 0, 0, 0)
+        try:
+            y = d_gemv("q4_0", x, wq, N, K)
+        finally:
+            g.call("smk_set_gemv_tuning", 0, 0, 0, 0)
+        np.testing.assert_array_equal(y.view(np.uint32), o.gemv_q4_0_simd(x, wq, N, K).view(np.uint32))
+
+    def test_config_1_shape(self):
+        x, w = o.synthetic(0, [(2048,), (8192, 2048)], [1.0, 0.02])
+        wq = o.quantize_q4_0(w)
+        y = d_gemv("q4_0", x, wq, 8192, 2048)
+        np.testing.assert_array_equal(y.view(np.uint32), o.gemv_q4_0_simd(x, wq, 8192, 2048).view(np.uint32))
+
+
 class TestBatched:
     @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
     @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])

@@ -479,3 +479,81 @@ class TestLlamaFormulas:
         mid = ~hi & ~lo
         s = (8192 / wl[mid] - 1.0) / 3.0
         np.testing.assert_allclose(sc[mid], (1 - s) * base[mid] / 32.0 + s * base[mid], rtol=1e-5)
+
+
+class TestReferenceSimdOrder:
+    """The oracle's restatements of the reference's SIMD-table arithmetic orders, pinned bit for
+    bit to the reference's own build (its widest table on this CPU: AVX-512 here; the Q4_0 loop,
+    SiLU and softmax are shared with the AVX2 table)."""
+
+    @pytest.fixture
+    def simd(self, ref_lib):
+        isa = o.ref_best_isa()
+        if isa not in ("avx2", "avx512"):
+            pytest.skip("the reference's SIMD tables need AVX2")
+        return ref_lib, o.ISA[isa]
+
+    @pytest.mark.parametrize("N,K", [(1, 32), (2, 64), (3, 64), (7, 96), (9, 2048), (17, 4096), (33, 11008),
+                                     (1001, 2048), (2048, 8192)])
+    def test_gemv_q4_0(self, simd, N, K):
+        R, isa = simd
+        rng = np.random.default_rng(N + K)
+        wq = o.quantize_q4_0((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+        x = (rng.standard_normal(K) * 3).astype(np.float32)
+        yr = np.empty(N, np.float32)
+        R.ref_gemv_q4_0(isa, N, K, x.ctypes.data_as(o._f32p), wq.ctypes.data_as(o._u8p), yr.ctypes.data_as(o._f32p))
+        np.testing.assert_array_equal(o.gemv_q4_0_simd(x, wq, N, K).view(np.uint32), yr.view(np.uint32))
+
+    def test_scalar_order_differs(self, simd):
+        """The scalar table's sequential sum is a different function: a planted-order check."""
+        R, isa = simd
+        rng = np.random.default_rng(1)
+        wq = o.quantize_q4_0((rng.standard_normal((512, 2048)) * 0.02).astype(np.float32))
+        x = rng.standard_normal(2048).astype(np.float32)
+        assert not np.array_equal(o.gemv_q4_0(x, wq, 512, 2048), o.gemv_q4_0_simd(x, wq, 512, 2048))
+
+    @pytest.mark.parametrize("M,N,K", [(4, 1, 64), (4, 160, 64), (1, 5, 100), (3, 7, 31), (8, 9, 200)])
+    def test_sgemm_trans_b_few_rows(self, simd, M, N, K):
+        R, isa = simd
+        rng = np.random.default_rng(M * N * K)
+        A = rng.standard_normal((M, K)).astype(np.float32)
+        B = rng.standard_normal((N, K)).astype(np.float32)
+        Cr = np.zeros((M, N), np.float32)
+        R.ref_sgemm(isa, 0, 1, M, N, K, 0.125, A.ctypes.data, K, B.ctypes.data, K, 0.0, Cr.ctypes.data_as(o._f32p), N)
+        np.testing.assert_array_equal(o.sgemm_tb_simd(A, B, 0.125).view(np.uint32), Cr.view(np.uint32))
+
+    @pytest.mark.parametrize("M,N,K", [(4, 64, 1), (4, 64, 37), (4, 64, 160), (3, 64, 100)])
+    def test_sgemm_direct(self, simd, M, N, K):
+        R, isa = simd
+        rng = np.random.default_rng(M + N + K)
+        A = np.abs(rng.standard_normal((M, K))).astype(np.float32)
+        B = rng.standard_normal((K, N)).astype(np.float32)
+        Cr = np.zeros((M, N), np.float32)
+        R.ref_sgemm(isa, 0, 0, M, N, K, 1.0, A.ctypes.data, K, B.ctypes.data, N, 0.0, Cr.ctypes.data_as(o._f32p), N)
+        np.testing.assert_array_equal(o.sgemm_nn_simd(A, B).view(np.uint32), Cr.view(np.uint32))
+
+    def test_silu(self, simd):
+        R, isa = simd
+        rng = np.random.default_rng(2)
+        x = np.concatenate([rng.standard_normal(100000) * 10, rng.uniform(-100, 100, 100000),
+                            np.array([0, -0.0, 88, -88, 88.5, -88.5, 1e30, -1e30, np.inf, -np.inf])]).astype(np.float32)
+        yr = np.empty_like(x)
+        R.ref_silu(isa, x.ctypes.data_as(o._f32p), yr.ctypes.data_as(o._f32p), x.size)
+        np.testing.assert_array_equal(o.silu_simd(x).view(np.uint32), yr.view(np.uint32))
+
+    def test_softmax(self, simd):
+        R, isa = simd
+        rng = np.random.default_rng(3)
+        for n in list(range(1, 40)) + [100, 127, 128, 129, 160, 1000]:
+            s = (rng.standard_normal(n) * rng.uniform(0.1, 20)).astype(np.float32)
+            r = np.empty_like(s)
+            R.ref_softmax_row(isa, s.ctypes.data_as(o._f32p), r.ctypes.data_as(o._f32p), n)
+            np.testing.assert_array_equal(o.softmax_simd(s).view(np.uint32), r.view(np.uint32), err_msg=str(n))
+
+    def test_fast_exp_accuracy(self):
+        """The restated exp against float64 (simd_math.hpp:57: absolute error <= 1.22e-7 on
+        [-87.3, 88.4] relative to values of order 1)."""
+        z = np.linspace(-10, 10, 20001).astype(np.float32)
+        got = np.array([o.lib().smko_fast_exp(float(v)) for v in z[::50]])
+        ref = np.exp(z[::50].astype(np.float64))
+        assert (np.abs(got - ref) / np.maximum(ref, 1) <= 2.5e-7).all()
