@@ -351,27 +351,40 @@ __global__ __launch_bounds__(NT) void gemv_pairs_kernel(int M, int N, int K, con
 // block's values {4k..4k+3} and {16+4k..16+4k+3} (minus 8 times x's sum over them) and adds
 // fma(float(dot), fp16(d) * dx, acc) block after block; y = (acc0 + acc2) + (acc1 + acc3).
 // The last row of an odd N (q4_row_single) keeps eight lanes, the low-nibble and high-nibble
-// halves apart, and sums them lane-wise first.  Integer dots are exact in any order, so:
+// halves apart, and sums them lane-wise first (handled by the generic kernel below, one row).
+// Integer dots are exact in any order, so for the even rows:
 //   phase 1 (parallel, as the pair kernel): a lane takes a 36-byte pair of one row and
-//     computes, for each block and each of the four reference lanes, the low-half and
-//     high-half integer dots (|dot| <= 4064: two int16 in one dword) and the block scale;
-//     they go to LDS, [row][block] with one padding entry per row (bank spread);
-//   phase 2: four lanes per row run the four FMA chains over the blocks in order, then DPP
-//     adds the lanes as the reference's horizontal sum does.
-__device__ __forceinline__ uint32_t pack_i16x2(int lo, int hi) {
-    return (static_cast<uint32_t>(lo) & 0xffffu) | (static_cast<uint32_t>(hi) << 16);
-}
+//     computes, for each block and each of the four reference lanes, that lane's integer dot
+//     and the block scale; they go to LDS, [row][lane][block] (chain-major);
+//   phase 2 (each wave for its own rows, no workgroup barrier): four lanes per row run the
+//     four FMA chains over the blocks in order, reading four blocks per 16-byte LDS load,
+//     then DPP adds the lanes as the reference's horizontal sum does.
+// Row stride (entries) of the phase-1 output: a multiple of 4 (16-byte reads of four blocks)
+// that is 4 mod 64, so the 16-byte reads of lanes (r, k) and (r, k + 1) fall 16 bytes apart
+// in the banks.
+__host__ __device__ __forceinline__ int ordered_stride(int nb) { return ((nb + 63) & ~63) + 4; }
 
-// Low and high integer dots of one reference lane: 4 quant bytes (nibble pairs) against x's
-// dword of values {4k..} (xl) and of values {16+4k..} (xh); -8 * sum(x) as the start.
-__device__ __forceinline__ uint32_t lane_dots(uint32_t q, uint32_t xl, uint32_t xh) {
+// Integer dot of one reference lane over its eight values: the block's 4 quant bytes (nibble
+// pairs) against x's dword of values {4k..} (xl) and of values {16+4k..} (xh), -8 * sum(x)
+// included.  Exact.
+__device__ __forceinline__ int lane_dot(uint32_t q, uint32_t xl, uint32_t xh) {
     constexpr uint32_t kMinus8 = 0xF8F8F8F8u;  // four int8 -8
-    const int dl = dot4(q & 0x0f0f0f0fu, xl, dot4(kMinus8, xl, 0));
-    const int dh = dot4((q >> 4) & 0x0f0f0f0fu, xh, dot4(kMinus8, xh, 0));
-    return pack_i16x2(dl, dh);
+    const int bias = dot4(kMinus8, xl, dot4(kMinus8, xh, 0));
+    return dot4(q & 0x0f0f0f0fu, xl, dot4((q >> 4) & 0x0f0f0f0fu, xh, bias));
 }
 
-template <int LPR, int MT, int NT>
+// Orders LDS accesses of one wave (writes by some lanes, then reads by others): a wave-scope
+// fence around a scheduling barrier; no workgroup barrier is needed.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// N even (an odd N's last row goes to the generic kernel, which keeps q4_row_single's order).
+// CH: pairs one lane takes per row (K/64 <= CH * LPR).  The weights of the next group of rows
+// (CH pairs per lane) are loaded while the current group's two phases run.
+template <int LPR, int MT, int NT, int CH>
 __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K, const float* __restrict__ x,
                                                              int ldx, const uint8_t* __restrict__ W,
                                                              float* __restrict__ y, int ldy, int rows_per_wg,
@@ -381,123 +394,138 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
     constexpr int kWaves = NT / kWave;
     constexpr int kRows = kWaves * G;        // rows of one group
     constexpr int PQ = (MT * 1024 + NT - 1) / NT < 4 ? (MT * 1024 + NT - 1) / NT : 4;
-    static_assert(4 * kRows <= NT, "phase 2 needs four lanes per row");
+    static_assert(4 * G * MT <= kWave, "phase 2 needs four lanes of the wave per row and row of x");
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ int bad[MT];
 
     const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
-    const int stride = nb + 1;
+    const int S = ordered_stride(nb);
     const size_t row_bytes = static_cast<size_t>(nb) * kQ4_0Bytes;
     uint32_t* lds_q = lds;                                              // M * quads
     float* lds_dx = reinterpret_cast<float*>(lds + M * quads);          // M * nb
     const int x_words = (M * (quads + nb) + 3) & ~3;
-    uint4* part = reinterpret_cast<uint4*>(lds + x_words);              // M * kRows * stride
-    float* scl = reinterpret_cast<float*>(part + M * kRows * stride);   // M * kRows * stride
+    int* part = reinterpret_cast<int*>(lds + x_words);                  // [M][kRows][4][S] lane dots
+    float* scl = reinterpret_cast<float*>(part + M * kRows * 4 * S);    // [M][kRows][S] scales
 
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int g = lane / LPR, j = lane % LPR;
     const int rl = wave * G + g;             // this lane's row within the group (phase 1)
     const int row0 = blockIdx.x * rows_per_wg;
     const int row_end = min(N, row0 + rows_per_wg);
-    const int chunks = (pairs + LPR - 1) / LPR;
     const int iters = (row_end - row0 + kRows - 1) / kRows;
-    const int steps = iters * chunks;
 
     if (threadIdx.x < MT) bad[threadIdx.x] = 0;
     lds_barrier();
 
-    auto load_step = [&](int s, uint32_t (&w)[D]) {
-        const int it = s / chunks, c = s - it * chunks;
-        const int p = min(j + c * LPR, pairs - 1);
+    // Unconditional loads from a clamped row and pair, so the compiler's wait counts stay exact.
+    auto load_group = [&](int it, uint32_t (&w)[CH][D]) {
         const int r = min(row0 + it * kRows + rl, row_end - 1);
-        load_pair<D>(W + r * row_bytes + static_cast<size_t>(p) * (2 * kQ4_0Bytes), w);
+        const uint8_t* base = W + r * row_bytes;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int p = min(j + c * LPR, pairs - 1);
+            load_pair<D>(base + static_cast<size_t>(p) * (2 * kQ4_0Bytes), w[c]);
+        }
     };
 
     XPreload<NT, PQ> xp;
     xp.load(x, ldx, M, K);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_sched_barrier(0);
-    uint32_t wa[D], wb[D];
-    load_step(0, wa);
+    uint32_t wa[CH][D], wb[CH][D];
+    load_group(0, wa);
     __builtin_amdgcn_sched_barrier(0);
     xp.template quantize<true, false>(x, ldx, M, K, lds_q, nullptr, lds_dx, bad);
     lds_barrier();
 
+    // Phase 1 of one pair: the four reference lanes' dots of both blocks, and the scales.
+    auto phase1 = [&](int p, const uint32_t (&w)[D]) {
+        uint32_t qa[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) qa[k] = skip2(w[k + 1], w[k]);
+        const float hA = half_bits_to_float(w[0]), hB = half_bits_to_float(w[4] >> 16);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m < M) {
+                const uint4* planes = reinterpret_cast<const uint4*>(lds_q + m * quads);
+                const uint4 x0 = planes[p], x1 = planes[pairs + p], x2 = planes[2 * pairs + p],
+                            x3 = planes[3 * pairs + p];
+                int* pr = part + (m * kRows + rl) * 4 * S + 2 * p;
+                *reinterpret_cast<int2*>(pr) = make_int2(lane_dot(qa[0], x0.x, x1.x), lane_dot(w[5], x2.x, x3.x));
+                *reinterpret_cast<int2*>(pr + S) = make_int2(lane_dot(qa[1], x0.y, x1.y), lane_dot(w[6], x2.y, x3.y));
+                *reinterpret_cast<int2*>(pr + 2 * S) = make_int2(lane_dot(qa[2], x0.z, x1.z), lane_dot(w[7], x2.z, x3.z));
+                *reinterpret_cast<int2*>(pr + 3 * S) = make_int2(lane_dot(qa[3], x0.w, x1.w), lane_dot(w[8], x2.w, x3.w));
+                const float2 d2 = *reinterpret_cast<const float2*>(lds_dx + m * nb + 2 * p);
+                *reinterpret_cast<float2*>(scl + (m * kRows + rl) * S + 2 * p) = make_float2(hA * d2.x, hB * d2.y);
+            }
+        }
+    };
+
+    // Phase 2 of one group, wave by wave: lane (m, g', k) of the wave runs reference lane k's
+    // chain for the wave's row g' against row m of x.
     auto phase2 = [&](int it) {
-        const int t = threadIdx.x;
-        if (t < 4 * kRows) {
-            const int r = t >> 2, k = t & 3;
+        if (lane < 4 * G * M) {
+            const int m = lane / (4 * G), rg = (lane >> 2) % G, k = lane & 3;
+            const int r = wave * G + rg;
             const int row = row0 + it * kRows + r;
-            const bool single = (N & 1) && row == N - 1;
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                if (m >= M) break;
-                const uint32_t* pv = reinterpret_cast<const uint32_t*>(part + (m * kRows + r) * stride) + k;
-                const float* sv = scl + (m * kRows + r) * stride;
-                float a1 = 0.0f, a2 = 0.0f;
-                for (int b = 0; b < nb; ++b) {
-                    const uint32_t v = pv[4 * b];
-                    const float s = sv[b];
-                    const int dl = static_cast<int16_t>(v & 0xffffu), dh = static_cast<int>(v) >> 16;
-                    a1 = fmaf(static_cast<float>(single ? dl : dl + dh), s, a1);
-                    a2 = fmaf(static_cast<float>(dh), s, a2);
-                }
-                float tt = single ? a1 + a2 : a1;
-                tt = tt + dpp_f<kDppQuadXor2>(tt);   // lanes k and k + 2
-                tt = tt + dpp_f<kDppQuadXor1>(tt);   // then the two pair sums
-                if (k == 0 && row < row_end) {
-                    float* yp = y + static_cast<size_t>(m) * ldy + row;
-                    *yp = bad[m] ? __builtin_nanf("") : (accumulate ? *yp + tt : tt);
-                }
+            const int4* pv = reinterpret_cast<const int4*>(part + ((m * kRows + r) * 4 + k) * S);
+            const float4* sv = reinterpret_cast<const float4*>(scl + (m * kRows + r) * S);
+            float a = 0.0f;
+            const int n4 = nb >> 2;
+            int q = 0;
+            for (; q + 1 < n4; q += 2) {
+                const int4 v0 = pv[q], v1 = pv[q + 1];
+                const float4 s0 = sv[q], s1 = sv[q + 1];
+                a = fmaf(static_cast<float>(v0.x), s0.x, a);
+                a = fmaf(static_cast<float>(v0.y), s0.y, a);
+                a = fmaf(static_cast<float>(v0.z), s0.z, a);
+                a = fmaf(static_cast<float>(v0.w), s0.w, a);
+                a = fmaf(static_cast<float>(v1.x), s1.x, a);
+                a = fmaf(static_cast<float>(v1.y), s1.y, a);
+                a = fmaf(static_cast<float>(v1.z), s1.z, a);
+                a = fmaf(static_cast<float>(v1.w), s1.w, a);
+            }
+            if (q < n4) {
+                const int4 v0 = pv[q];
+                const float4 s0 = sv[q];
+                a = fmaf(static_cast<float>(v0.x), s0.x, a);
+                a = fmaf(static_cast<float>(v0.y), s0.y, a);
+                a = fmaf(static_cast<float>(v0.z), s0.z, a);
+                a = fmaf(static_cast<float>(v0.w), s0.w, a);
+            }
+            if (nb & 2) {  // nb is even: at most two blocks left
+                const int4 v0 = pv[n4];
+                const float4 s0 = sv[n4];
+                a = fmaf(static_cast<float>(v0.x), s0.x, a);
+                a = fmaf(static_cast<float>(v0.y), s0.y, a);
+            }
+            a = a + dpp_f<kDppQuadXor2>(a);   // lanes k and k + 2
+            a = a + dpp_f<kDppQuadXor1>(a);   // then the two pair sums
+            if (k == 0 && row < row_end) {
+                float* yp = y + static_cast<size_t>(m) * ldy + row;
+                *yp = bad[m] ? __builtin_nanf("") : (accumulate ? *yp + a : a);
             }
         }
     };
 
-    auto body = [&](int s, uint32_t (&cur)[D], uint32_t (&nxt)[D]) {
-        load_step(s + 1 < steps ? s + 1 : s, nxt);
-        const int it = s / chunks, c = s - it * chunks;
-        const int p = j + c * LPR;
-        if (p < pairs) {
-            uint32_t qa[4];
+    auto body = [&](int it, uint32_t (&cur)[CH][D], uint32_t (&nxt)[CH][D]) {
+        load_group(it + 1 < iters ? it + 1 : it, nxt);  // the last group reloads its own (cached) bytes
 #pragma unroll
-            for (int k = 0; k < 4; ++k) qa[k] = skip2(cur[k + 1], cur[k]);
-            const float hA = half_bits_to_float(cur[0]), hB = half_bits_to_float(cur[4] >> 16);
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                if (m < M) {
-                    const uint4* planes = reinterpret_cast<const uint4*>(lds_q + m * quads);
-                    const uint4 x0 = planes[p], x1 = planes[pairs + p], x2 = planes[2 * pairs + p],
-                                x3 = planes[3 * pairs + p];
-                    uint4 pa, pb;
-                    pa.x = lane_dots(qa[0], x0.x, x1.x);
-                    pa.y = lane_dots(qa[1], x0.y, x1.y);
-                    pa.z = lane_dots(qa[2], x0.z, x1.z);
-                    pa.w = lane_dots(qa[3], x0.w, x1.w);
-                    pb.x = lane_dots(cur[5], x2.x, x3.x);
-                    pb.y = lane_dots(cur[6], x2.y, x3.y);
-                    pb.z = lane_dots(cur[7], x2.z, x3.z);
-                    pb.w = lane_dots(cur[8], x2.w, x3.w);
-                    const int e = (m * kRows + rl) * stride + 2 * p;
-                    part[e] = pa;
-                    part[e + 1] = pb;
-                    scl[e] = hA * lds_dx[m * nb + 2 * p];
-                    scl[e + 1] = hB * lds_dx[m * nb + 2 * p + 1];
-                }
-            }
+        for (int c = 0; c < CH; ++c) {
+            const int p = j + c * LPR;
+            if (p < pairs) phase1(p, cur[c]);
         }
-        if (c == chunks - 1) {
-            lds_barrier();  // the group's partials are in LDS
-            phase2(it);
-            lds_barrier();  // read before the next group overwrites them
-        }
+        wave_lds_sync();  // this wave's rows are complete in LDS
+        phase2(it);
+        wave_lds_sync();  // read before the next group overwrites them
     };
 
-    int s = 0;
-    for (; s + 1 < steps; s += 2) {
-        body(s, wa, wb);
-        body(s + 1, wb, wa);
+    int it = 0;
+    for (; it + 1 < iters; it += 2) {
+        body(it, wa, wb);
+        body(it + 1, wb, wa);
     }
-    if (s < steps) body(s, wa, wb);
+    if (it < iters) body(it, wa, wb);
 }
 
 // Odd K/32 or a 2-byte aligned W: four lanes per row walk the blocks themselves (16-bit
@@ -533,8 +561,9 @@ __global__ __launch_bounds__(kThreads) void gemv_q4_ordered_generic_kernel(int M
         for (int m = 0; m < MT; ++m) {
             if (m >= M) break;
             const uint32_t* xb = lds_q + m * quads + 8 * b;
-            const uint32_t v = lane_dots(q, xb[k], xb[4 + k]);
-            const int dl = static_cast<int16_t>(v & 0xffffu), dh = static_cast<int>(v) >> 16;
+            constexpr uint32_t kMinus8 = 0xF8F8F8F8u;
+            const int dl = dot4(q & 0x0f0f0f0fu, xb[k], dot4(kMinus8, xb[k], 0));
+            const int dh = dot4((q >> 4) & 0x0f0f0f0fu, xb[4 + k], dot4(kMinus8, xb[4 + k], 0));
             const float s = hd * lds_dx[m * nb + b];
             a1[m] = fmaf(static_cast<float>(single ? dl : dl + dh), s, a1[m]);
             a2[m] = fmaf(static_cast<float>(dh), s, a2[m]);
@@ -744,20 +773,32 @@ hipError_t launch_generic(int M, int N, int K, const float* x, int ldx, const ui
 size_t ordered_lds_bytes(int M, int K, int rows_per_group) {
     const size_t nb = static_cast<size_t>(K) >> 5, quads = static_cast<size_t>(K) >> 2;
     const size_t x_words = (M * (quads + nb) + 3) & ~static_cast<size_t>(3);
-    return 4 * x_words + static_cast<size_t>(M) * rows_per_group * (nb + 1) * 20;
+    return 4 * x_words + static_cast<size_t>(M) * rows_per_group * ordered_stride(static_cast<int>(nb)) * 20;
 }
 
-template <int LPR, int MT, int NT>
-hipError_t launch_ordered(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
-                          int rows_per_wg, int acc, hipStream_t stream) {
+template <int LPR, int MT, int NT, int CH>
+hipError_t launch_ordered_ch(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
+                             int rows_per_wg, int acc, hipStream_t stream) {
     constexpr int kRows = NT / LPR;
     const size_t lds = ordered_lds_bytes(M, K, kRows);
     if (rows_per_wg <= 0) rows_per_wg = std::max(kRows, (N + 511) / 512);
     const int grid = (N + rows_per_wg - 1) / rows_per_wg;
-    if (const hipError_t e = allow_lds(gemv_q4_ordered_kernel<LPR, MT, NT>, lds); e != hipSuccess) return e;
-    hipLaunchKernelGGL((gemv_q4_ordered_kernel<LPR, MT, NT>), dim3(grid), dim3(NT), lds, stream, M, N, K, x, ldx, W, y,
-                       ldy, rows_per_wg, acc);
+    if (const hipError_t e = allow_lds(gemv_q4_ordered_kernel<LPR, MT, NT, CH>, lds); e != hipSuccess) return e;
+    hipLaunchKernelGGL((gemv_q4_ordered_kernel<LPR, MT, NT, CH>), dim3(grid), dim3(NT), lds, stream, M, N, K, x, ldx,
+                       W, y, ldy, rows_per_wg, acc);
     return hipGetLastError();
+}
+
+// Pairs per lane and row: 1, 2, 4 or 8 (the lane split is raised until that suffices).
+template <int LPR, int MT, int NT>
+hipError_t launch_ordered(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
+                          int rows_per_wg, int acc, hipStream_t stream) {
+    const int chunks = ((K >> 6) + LPR - 1) / LPR;
+    if (chunks <= 1) return launch_ordered_ch<LPR, MT, NT, 1>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, stream);
+    if (chunks <= 2) return launch_ordered_ch<LPR, MT, NT, 2>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, stream);
+    if (chunks <= 4) return launch_ordered_ch<LPR, MT, NT, 4>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, stream);
+    if (chunks <= 8) return launch_ordered_ch<LPR, MT, NT, 8>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, stream);
+    return hipErrorInvalidValue;
 }
 
 template <int MT, int NT>
@@ -788,7 +829,21 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
     const int acc = t ? t->accumulate : 0;
     const int pairs = (K >> 5) / 2;
     constexpr size_t kLdsCap = 150 * 1024;
-    const bool generic = !pair_path_ok(K, W) || ordered_lds_bytes(M, K, 256 / 64) > kLdsCap;
+    const bool generic = !pair_path_ok(K, W) || ordered_lds_bytes(M, K, 256 / 64) > kLdsCap || pairs > 8 * 64;
+    if (!generic && (N & 1)) {
+        // The last row of an odd N has its own order (q4_row_single): one row through the
+        // generic kernel, the even rest through the pair kernel.
+        const size_t row_bytes = static_cast<size_t>(K >> 5) * kQ4_0Bytes;
+        hipError_t e = hipSuccess;
+        switch (mt) {
+            case 1: e = launch_ordered_generic<1>(M, 1, K, x, ldx, W + (N - 1) * row_bytes, y + (N - 1), ldy, acc, stream); break;
+            case 2: e = launch_ordered_generic<2>(M, 1, K, x, ldx, W + (N - 1) * row_bytes, y + (N - 1), ldy, acc, stream); break;
+            case 4: e = launch_ordered_generic<4>(M, 1, K, x, ldx, W + (N - 1) * row_bytes, y + (N - 1), ldy, acc, stream); break;
+            default: e = launch_ordered_generic<8>(M, 1, K, x, ldx, W + (N - 1) * row_bytes, y + (N - 1), ldy, acc, stream); break;
+        }
+        if (e != hipSuccess || N == 1) return e;
+        --N;
+    }
     if (generic) {
         switch (mt) {
             case 1: return launch_ordered_generic<1>(M, N, K, x, ldx, W, y, ldy, acc, stream);
@@ -799,7 +854,8 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
     }
     // The lane split does not change the result here (every row's sum has the reference's
     // order), so it is chosen for speed only.
-    int lpr = (t && t->lanes_per_row) ? t->lanes_per_row : (pairs >= 128 ? 64 : pairs >= 32 ? 32 : pairs >= 16 ? 16 : 8);
+    int lpr = (t && t->lanes_per_row) ? t->lanes_per_row : (pairs >= 128 ? 64 : pairs >= 16 ? 16 : 8);
+    while (lpr < 64 && (pairs + lpr - 1) / lpr > 8) lpr *= 2;  // at most 8 pairs per lane and row
     int rpw = t ? t->rows_per_wg : 0;
     if (mt == 1) {
         const double bytes = static_cast<double>(N) * (K >> 5) * kQ4_0Bytes;
@@ -817,11 +873,15 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
             default: return launch_ordered_lpr<1, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
         }
     }
-    lpr = ordered_lds_bytes(M, K, 256 / 32) <= kLdsCap && lpr <= 32 ? 32 : 64;
+    // Several rows of x: 256 threads, 32 or 64 lanes per row (phase 2 needs 4 * rows * M lanes).
+    const bool l32 = ordered_lds_bytes(M, K, 256 / 32) <= kLdsCap && lpr <= 32;
     switch (mt) {
-        case 2: return launch_ordered_lpr<2, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
-        case 4: return launch_ordered_lpr<4, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
-        default: return launch_ordered_lpr<8, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
+        case 2: return l32 ? launch_ordered<32, 2, 256>(M, N, K, x, ldx, W, y, ldy, rpw, acc, stream)
+                           : launch_ordered<64, 2, 256>(M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
+        case 4: return l32 ? launch_ordered<32, 4, 256>(M, N, K, x, ldx, W, y, ldy, rpw, acc, stream)
+                           : launch_ordered<64, 4, 256>(M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
+        default: return l32 ? launch_ordered<32, 8, 256>(M, N, K, x, ldx, W, y, ldy, rpw, acc, stream)
+                            : launch_ordered<64, 8, 256>(M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
     }
 }
 
