@@ -159,6 +159,11 @@ int smk_llama_step(void* model, int token, float* logits);
  * out: the n_new generated ids; seconds (optional, 2 doubles): prefill and decode time. */
 int smk_llama_generate(void* model, const int* prompt, int n_prompt, int n_new, int* out, double* seconds);
 int smk_llama_info(void* model, int* position, int* capacity, unsigned long long* weight_bytes);
+/* step() run eagerly with a HIP event at every section start (the engine's counterpart of
+ * llama.py:441-479, _step_profiled); adds each section's milliseconds into section_ms[0..11):
+ * embed, rms_norm, gemv_qkv, rope_kv, attention, gemv_o, gemv_gate_up, silu_mul, gemv_down,
+ * lm_head, argmax.  Launch gaps between sections are included. */
+int smk_llama_step_profile(void* model, int token, float* logits, double* section_ms, int n_sections);
 
 /* Device memory, copies, streams, events and graphs, for callers without their own runtime
  * objects (the tests and bench.py use these; no other framework is loaded with the library). */

@@ -21,6 +21,7 @@
 #include "abi_internal.hpp"
 #include "device_common.hpp"
 #include "launch.hpp"
+#include "pairwise_sum.hpp"
 #include "smk_hip.h"
 
 #include <algorithm>
@@ -33,7 +34,7 @@ namespace smk {
 namespace {
 
 constexpr int kGgmlF32 = 0, kGgmlQ4_0 = 2, kGgmlQ8_0 = 8;
-constexpr int kMaxCapacity = 32768;  // attention scores of one head live in LDS
+constexpr int kMaxCapacity = 16384;  // attention scores of one head live in LDS
 
 struct DecodeState {
     int pos;       // position of the next step
@@ -121,8 +122,31 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, const float* __restrict_
 //     of 8, eight running double sums, a double exp on the last n % 8);
 //   out = sk.sgemm(p, V): the AVX2 direct product (avx2_gemm_packed.cpp:151-201), one fused
 //     chain over the positions in order per output.
-// One workgroup of 256 threads per head; scores in LDS.
+// One workgroup of 256 threads per head; scores in LDS; K and V read in tiles of kTile
+// positions staged through LDS with coalesced loads.
 constexpr int kAttnThreads = 256;
+constexpr int kTile = 64;
+
+// count floats (a multiple of 4, 16-byte aligned ends) from global to LDS: every thread issues
+// its four 16-byte loads of a round before storing any (no load waits for an earlier store).
+__device__ __forceinline__ void stage_tile(float* __restrict__ dst, const float* __restrict__ src, int count) {
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+    float4* d4 = reinterpret_cast<float4*>(dst);
+    const int n4 = count >> 2;
+    for (int base = 0; base < n4; base += 4 * kAttnThreads) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = base + u * kAttnThreads + static_cast<int>(threadIdx.x);
+            v[u] = s4[e < n4 ? e : 0];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = base + u * kAttnThreads + static_cast<int>(threadIdx.x);
+            if (e < n4) d4[e] = v[u];
+        }
+    }
+}
 
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __restrict__ q_all,
                                                                  const float* __restrict__ kc,
@@ -130,39 +154,44 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
                                                                  int hd, int cap, float scale,
                                                                  const DecodeState* __restrict__ st,
                                                                  float* __restrict__ out) {
-    extern __shared__ float sc[];  // T scores, then probabilities
+    extern __shared__ float sc[];  // T scores, then probabilities; then the K / V tile
     __shared__ float qs[256];
     __shared__ float red_f[kAttnThreads / kWave];
     __shared__ int red_i[kAttnThreads / kWave];
     __shared__ double lane_sum[8];
-    __shared__ float tail_d[8];
+    __shared__ double tail_e[8];
     __shared__ float inv_s;
     const int head = blockIdx.x;
     const int g = head / (n_heads / n_kv);
     const int T = st->pos + 1;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     constexpr int kWaves = kAttnThreads / kWave;
+    float* tile = sc + ((cap + 3) & ~3);  // kTile * hd floats
     for (int d = threadIdx.x; d < hd; d += kAttnThreads) qs[d] = q_all[static_cast<size_t>(head) * hd + d];
-    __syncthreads();
     const float* K = kc + static_cast<size_t>(g) * cap * hd;
     const float* V = vc + static_cast<size_t>(g) * cap * hd;
-    // Scores: 16 lanes per position.
+    // Scores, a tile of positions at a time: 16 lanes per position.
     const int l = threadIdx.x & 15;
-    for (int t0 = 0; t0 < T; t0 += kAttnThreads / 16) {
-        const int t = t0 + static_cast<int>(threadIdx.x >> 4);
-        const int tt = min(t, T - 1);
-        const float* kr = K + static_cast<size_t>(tt) * hd;
-        float a0 = 0.0f, a1 = 0.0f;
-        for (int p = 0; p < hd; p += 32) {
-            if (p + l < hd) a0 = fmaf(qs[p + l], kr[p + l], a0);
-            if (p + 16 + l < hd) a1 = fmaf(qs[p + 16 + l], kr[p + 16 + l], a1);
+    for (int t0 = 0; t0 < T; t0 += kTile) {
+        const int tn = min(kTile, T - t0);
+        __syncthreads();  // the previous tile is consumed (and qs is written, first time)
+        stage_tile(tile, K + static_cast<size_t>(t0) * hd, tn * hd);
+        __syncthreads();
+        for (int tt = threadIdx.x >> 4; tt < kTile; tt += kAttnThreads / 16) {
+            const int tc = min(tt, tn - 1);
+            const float* kr = tile + tc * hd;
+            float a0 = 0.0f, a1 = 0.0f;
+            for (int p = 0; p < hd; p += 32) {
+                if (p + l < hd) a0 = fmaf(qs[p + l], kr[p + l], a0);
+                if (p + 16 + l < hd) a1 = fmaf(qs[p + 16 + l], kr[p + 16 + l], a1);
+            }
+            float v = a0 + a1;
+            v = v + __shfl_xor(v, 8, 16);
+            v = v + __shfl_xor(v, 4, 16);
+            v = v + __shfl_xor(v, 2, 16);
+            v = v + __shfl_xor(v, 1, 16);
+            if (l == 0 && tt < tn) sc[t0 + tt] = scale * v;
         }
-        float v = a0 + a1;
-        v = v + __shfl_xor(v, 8, 16);
-        v = v + __shfl_xor(v, 4, 16);
-        v = v + __shfl_xor(v, 2, 16);
-        v = v + __shfl_xor(v, 1, 16);
-        if (l == 0 && t < T) sc[t] = scale * v;
     }
     __syncthreads();
     // Softmax over the T scores.
@@ -190,8 +219,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     const int n8 = T - T % 8;
     for (int t = threadIdx.x; t < T; t += kAttnThreads) {
         const float dd = sc[t] - mx;
-        if (t >= n8) tail_d[t - n8] = dd;
-        sc[t] = t < n8 ? exp_cody_waite(dd) : static_cast<float>(exp(static_cast<double>(dd)));
+        if (t < n8) {
+            sc[t] = exp_cody_waite(dd);
+        } else {
+            const double e = exp(static_cast<double>(dd));
+            tail_e[t - n8] = e;
+            sc[t] = static_cast<float>(e);
+        }
     }
     __syncthreads();
     if (threadIdx.x < 8) {
@@ -204,20 +238,27 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
         double tsum = lane_sum[0];
         for (int k = 1; k < 8; ++k) tsum = tsum + lane_sum[k];
         double sum = 0.0 + tsum;
-        for (int t = 0; t < T - n8; ++t) sum = sum + exp(static_cast<double>(tail_d[t]));
+        for (int t = 0; t < T - n8; ++t) sum = sum + tail_e[t];
         inv_s = static_cast<float>(1.0 / sum);
     }
     __syncthreads();
     const float inv = inv_s;
     for (int t = threadIdx.x; t < T; t += kAttnThreads) sc[t] = nan_row ? __builtin_nanf("") : sc[t] * inv;
-    __syncthreads();
-    // out[d] = one fused chain over the positions in order.
-    for (int d = threadIdx.x; d < hd; d += kAttnThreads) {
-        float acc = 0.0f;
-        for (int t = 0; t < T; ++t) acc = fmaf(sc[t], V[static_cast<size_t>(t) * hd + d], acc);
-        out[static_cast<size_t>(head) * hd + d] = acc;
+    // out[d] = one fused chain over the positions in order, V staged a tile at a time.
+    float acc = 0.0f;
+    const int d = threadIdx.x;
+    for (int t0 = 0; t0 < T; t0 += kTile) {
+        const int tn = min(kTile, T - t0);
+        __syncthreads();  // probabilities written / the previous tile consumed
+        stage_tile(tile, V + static_cast<size_t>(t0) * hd, tn * hd);
+        __syncthreads();
+        if (d < hd)
+            for (int t = 0; t < tn; ++t) acc = fmaf(sc[t0 + t], tile[t * hd + d], acc);
     }
+    if (d < hd) out[static_cast<size_t>(head) * hd + d] = acc;
 }
+
+size_t attention_lds(int cap, int hd) { return (static_cast<size_t>((cap + 3) & ~3) + static_cast<size_t>(kTile) * hd) * 4; }
 
 // m = silu(g) * u (llama.py:434: sk.silu(gate) * up, two float32 results multiplied), SiLU as
 // the reference's SIMD tables compute it.
@@ -234,24 +275,14 @@ __device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
     return a > b || (a == b && ia < ib);
 }
 
-// Greedy next token from the logits, then the position advances.  tokens[pos + 1] is written
-// only past the given prompt.
-constexpr int kArgmaxThreads = 1024;
+// Greedy next token in two stages: kArgmaxParts workgroups take contiguous slices of the
+// logits, then one wave merges their (value, index) candidates -- np.argmax's rule is
+// preserved because `better` breaks ties by the smaller index -- writes tokens[pos + 1] (only
+// past the given prompt) and advances the position.
+constexpr int kArgmaxParts = 128;
+constexpr int kArgmaxThreads = 256;
 
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, int n,
-                                                                int* __restrict__ tokens, int cap,
-                                                                DecodeState* __restrict__ st) {
-    __shared__ float bv[kArgmaxThreads / kWave];
-    __shared__ int bi[kArgmaxThreads / kWave];
-    float v = -__builtin_inff();
-    int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += kArgmaxThreads) {
-        const float c = logits[i];
-        if (better(c, i, v, idx)) {
-            v = c;
-            idx = i;
-        }
-    }
+__device__ __forceinline__ void argmax_wave(float& v, int& idx) {
     for (int off = kWave / 2; off > 0; off >>= 1) {
         const float ov = __shfl_xor(v, off, kWave);
         const int oi = __shfl_xor(idx, off, kWave);
@@ -260,6 +291,24 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
             idx = oi;
         }
     }
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_part_kernel(const float* __restrict__ logits, int n,
+                                                                     float* __restrict__ pv, int* __restrict__ pi) {
+    __shared__ float bv[kArgmaxThreads / kWave];
+    __shared__ int bi[kArgmaxThreads / kWave];
+    const int chunk = (n + gridDim.x - 1) / gridDim.x;
+    const int lo = blockIdx.x * chunk, hi = min(n, lo + chunk);
+    float v = -__builtin_inff();
+    int idx = 0x7fffffff;
+    for (int i = lo + threadIdx.x; i < hi; i += kArgmaxThreads) {
+        const float c = logits[i];
+        if (better(c, i, v, idx)) {
+            v = c;
+            idx = i;
+        }
+    }
+    argmax_wave(v, idx);
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     if (lane == 0) {
         bv[wave] = v;
@@ -272,6 +321,23 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
                 v = bv[w];
                 idx = bi[w];
             }
+        pv[blockIdx.x] = v;
+        pi[blockIdx.x] = idx;
+    }
+}
+
+__global__ __launch_bounds__(kWave) void argmax_final_kernel(const float* __restrict__ pv, const int* __restrict__ pi,
+                                                             int parts, int n, int* __restrict__ tokens, int cap,
+                                                             DecodeState* __restrict__ st) {
+    float v = -__builtin_inff();
+    int idx = 0x7fffffff;
+    for (int b = threadIdx.x; b < parts; b += kWave)
+        if (better(pv[b], pi[b], v, idx)) {
+            v = pv[b];
+            idx = pi[b];
+        }
+    argmax_wave(v, idx);
+    if (threadIdx.x == 0) {
         if (idx < 0 || idx >= n) idx = 0;  // n == 0 cannot happen (vocab > 0)
         const int p = st->pos;
         if (p + 1 >= st->n_prompt && p + 1 <= cap) tokens[p + 1] = idx;
@@ -305,6 +371,25 @@ struct Layer {
     Mat qkv, o, gateup, down;
 };
 
+// Section marks of a profiled (eager) step: an event recorded at each section start; the time
+// up to the next mark is the section's.  Sections: see smk_llama_step_profile.
+enum Section { kEmbed = 0, kRms, kGemvQkv, kRopeKv, kAttention, kGemvO, kGemvGateUp, kSiluMul, kGemvDown,
+               kLmHead, kArgmax, kSections };
+
+struct Marks {
+    std::vector<hipEvent_t> ev;
+    std::vector<int> id;
+    hipError_t mark(hipStream_t s, int section) {
+        if (id.size() == ev.size()) {
+            hipEvent_t e;
+            if (const hipError_t r = hipEventCreate(&e); r != hipSuccess) return r;
+            ev.push_back(e);
+        }
+        id.push_back(section);
+        return hipEventRecord(ev[id.size() - 1], s);
+    }
+};
+
 struct Model {
     smk_llama_config cfg{};
     hipStream_t stream = nullptr;
@@ -317,6 +402,8 @@ struct Model {
     float *x = nullptr, *h = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *m = nullptr,
           *logits = nullptr;
     DecodeState* st = nullptr;
+    float* part_v = nullptr;     // argmax candidates
+    int* part_i = nullptr;
     int* host_pinned = nullptr;  // staging for tokens and state
     // per capacity
     int capacity = 0;
@@ -325,7 +412,9 @@ struct Model {
     float *kc = nullptr, *vc = nullptr, *cos_tab = nullptr, *sin_tab = nullptr;
     hipGraphExec_t g_logits = nullptr, g_plain = nullptr;
     std::vector<unsigned> loaded;  // bit per tensor per layer
+    bool fuse_norm = false;        // Q4_0 GEMVs normalize x themselves
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    Marks marks;
     uint64_t weight_bytes = 0;
 
     int q_rows() const { return cfg.n_heads * cfg.head_dim; }
@@ -351,6 +440,23 @@ void free_capacity(Model& md) {
     md.capacity = 0;
 }
 
+// y (+)= RMSNorm(x, nw) . W^T: the Q4_0 GEMV normalizes x in its own prologue when the model
+// allows it (fuse_norm), else the RMSNorm kernel writes h first.
+hipError_t gemv(const Mat& W, const float* x, float* y, bool accumulate, hipStream_t s);
+
+hipError_t gemv_normed(const Model& md, const Mat& W, const float* x, const float* nw, float* h, float* y,
+                       bool accumulate) {
+    if (md.fuse_norm && W.type == kGgmlQ4_0) {
+        GemvTuning t;
+        t.accumulate = accumulate ? 1 : 0;
+        t.norm_w = nw;
+        t.norm_eps = md.cfg.rms_eps;
+        return gemv_quant(kQ4_0Bytes, 1, W.rows, W.cols, x, W.cols, W.p, y, W.rows, md.stream, &t);
+    }
+    if (const hipError_t e = rms_norm(x, nw, h, 1, md.cfg.hidden, md.cfg.rms_eps, md.stream); e != hipSuccess) return e;
+    return gemv(W, h, y, accumulate, md.stream);
+}
+
 hipError_t gemv(const Mat& W, const float* x, float* y, bool accumulate, hipStream_t s) {
     if (W.type == kGgmlF32)
         return gemm_tb(0, 1, W.rows, W.cols, 1.0f, x, W.cols, W.p, W.cols, accumulate ? 1.0f : 0.0f, y, W.rows, s);
@@ -360,10 +466,17 @@ hipError_t gemv(const Mat& W, const float* x, float* y, bool accumulate, hipStre
 }
 
 // Enqueue one decode step (the body every graph captures).
-hipError_t enqueue_step(Model& md, bool with_logits) {
+#define SMK_MARK(section)                                                         \
+    do {                                                                          \
+        if (mk)                                                                   \
+            if (const hipError_t e_ = mk->mark(s, section); e_ != hipSuccess) return e_; \
+    } while (0)
+
+hipError_t enqueue_step(Model& md, bool with_logits, Marks* mk = nullptr) {
     const smk_llama_config& c = md.cfg;
     hipStream_t s = md.stream;
     const int nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
+    SMK_MARK(kEmbed);
     hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, md.embed.p, md.embed.type, c.hidden, c.vocab,
                        md.tokens, md.st, md.x);
     if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
@@ -374,33 +487,42 @@ hipError_t enqueue_step(Model& md, bool with_logits) {
         const Layer& L = md.layers[l];
         float* kc = md.kc + l * layer_kv;
         float* vc = md.vc + l * layer_kv;
-        hipError_t e = rms_norm(md.x, L.attn_norm, md.h, 1, c.hidden, c.rms_eps, s);
-        if (e == hipSuccess) e = gemv(L.qkv, md.h, md.qkv, false, s);
+        SMK_MARK(kGemvQkv);
+        hipError_t e = gemv_normed(md, L.qkv, md.x, L.attn_norm, md.h, md.qkv, false);
         if (e != hipSuccess) return e;
+        SMK_MARK(kRopeKv);
         hipLaunchKernelGGL(rope_kv_kernel, dim3((rope_total + 255) / 256), dim3(256), 0, s, md.qkv, md.cos_tab,
                            md.sin_tab, nh, nkv, hd, c.rope_interleaved, kc, vc, md.capacity, md.st);
-        hipLaunchKernelGGL(attention_kernel, dim3(nh), dim3(kAttnThreads), static_cast<size_t>(md.capacity) * 4, s,
+        SMK_MARK(kAttention);
+        hipLaunchKernelGGL(attention_kernel, dim3(nh), dim3(kAttnThreads), attention_lds(md.capacity, hd), s,
                            md.qkv, kc, vc, nh, nkv, hd, md.capacity, scale, md.st, md.attn);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        e = gemv(L.o, md.attn, md.x, true, s);
-        if (e == hipSuccess) e = rms_norm(md.x, L.ffn_norm, md.h, 1, c.hidden, c.rms_eps, s);
-        if (e == hipSuccess) e = gemv(L.gateup, md.h, md.gu, false, s);
-        if (e != hipSuccess) return e;
+        SMK_MARK(kGemvO);
+        if ((e = gemv(L.o, md.attn, md.x, true, s)) != hipSuccess) return e;
+        SMK_MARK(kGemvGateUp);
+        if ((e = gemv_normed(md, L.gateup, md.x, L.ffn_norm, md.h, md.gu, false)) != hipSuccess) return e;
+        SMK_MARK(kSiluMul);
         hipLaunchKernelGGL(silu_mul_kernel, dim3((c.ffn + 255) / 256), dim3(256), 0, s, md.gu, c.ffn, md.m);
         if ((e = hipGetLastError()) != hipSuccess) return e;
+        SMK_MARK(kGemvDown);
         if ((e = gemv(L.down, md.m, md.x, true, s)) != hipSuccess) return e;
     }
     if (!with_logits) {
+        SMK_MARK(kArgmax);
         hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, s, md.st);
         return hipGetLastError();
     }
-    hipError_t e = rms_norm(md.x, md.out_norm, md.h, 1, c.hidden, c.rms_eps, s);
-    if (e == hipSuccess) e = gemv(md.head, md.h, md.logits, false, s);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, md.logits, c.vocab, md.tokens,
-                       md.capacity, md.st);
+    SMK_MARK(kLmHead);
+    if (const hipError_t e = gemv_normed(md, md.head, md.x, md.out_norm, md.h, md.logits, false); e != hipSuccess)
+        return e;
+    SMK_MARK(kArgmax);
+    hipLaunchKernelGGL(argmax_part_kernel, dim3(kArgmaxParts), dim3(kArgmaxThreads), 0, s, md.logits, c.vocab,
+                       md.part_v, md.part_i);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kWave), 0, s, md.part_v, md.part_i, kArgmaxParts, c.vocab,
+                       md.tokens, md.capacity, md.st);
     return hipGetLastError();
 }
+#undef SMK_MARK
 
 hipError_t capture(Model& md, bool with_logits, hipGraphExec_t* out) {
     hipError_t e = hipStreamBeginCapture(md.stream, hipStreamCaptureModeThreadLocal);
@@ -448,7 +570,7 @@ int smk_llama_create(const smk_llama_config* cfg, void** model) {
         c.vocab <= 0)
         return fail(SMK_ERR_ARGUMENT, "every dimension must be positive");
     if (c.n_heads % c.n_kv_heads) return fail(SMK_ERR_ARGUMENT, "n_heads must be a multiple of n_kv_heads");
-    if (c.head_dim % 2 || c.head_dim > 256) return fail(SMK_ERR_ARGUMENT, "head_dim must be even and <= 256");
+    if (c.head_dim % 4 || c.head_dim > 256) return fail(SMK_ERR_ARGUMENT, "head_dim must be a multiple of 4 and <= 256");
     if (c.hidden % 32 || c.ffn % 32 || (c.n_heads * c.head_dim) % 32)
         return fail(SMK_ERR_ARGUMENT, "hidden, ffn and n_heads*head_dim must be multiples of 32");
     for (int t : {c.matrix_type, c.embed_type})
@@ -491,6 +613,8 @@ int smk_llama_create(const smk_llama_config* cfg, void** model) {
         {reinterpret_cast<void**>(&md->m), static_cast<size_t>(c.ffn) * 4},
         {reinterpret_cast<void**>(&md->logits), static_cast<size_t>(c.vocab) * 4},
         {reinterpret_cast<void**>(&md->st), sizeof(DecodeState)},
+        {reinterpret_cast<void**>(&md->part_v), static_cast<size_t>(kArgmaxParts) * 4},
+        {reinterpret_cast<void**>(&md->part_i), static_cast<size_t>(kArgmaxParts) * 4},
     };
     if (!md->tied) want.push_back({reinterpret_cast<void**>(&md->head.p), md->head.bytes()});
     md->layers.resize(c.n_layers);
@@ -506,6 +630,11 @@ int smk_llama_create(const smk_llama_config* cfg, void** model) {
     for (const Want& w : want)
         if ((e = dalloc(*md, w.p, w.bytes)) != hipSuccess) return cleanup(e, "model allocation");
     if (md->tied) md->head = md->embed;
+    {
+        const int depth = uniform_depth(c.hidden);
+        md->fuse_norm = c.hidden <= 8192 && c.hidden % 64 == 0 && depth >= 0 && (8 << depth) <= 1024 &&
+                        (md->q_rows() + 2 * md->kv_rows()) % 2 == 0 && c.ffn % 2 == 0 && c.vocab % 2 == 0;
+    }
     md->weight_bytes = md->head.bytes();
     for (const Layer& L : md->layers) md->weight_bytes += L.qkv.bytes() + L.o.bytes() + L.gateup.bytes() + L.down.bytes();
     *model = md;
@@ -521,6 +650,7 @@ int smk_llama_destroy(void* model) {
     for (void* p : md->allocs) (void)hipFree(p);
     for (hipEvent_t& ev : md->ev)
         if (ev) (void)hipEventDestroy(ev);
+    for (hipEvent_t ev : md->marks.ev) (void)hipEventDestroy(ev);
     if (md->host_pinned) (void)hipHostFree(md->host_pinned);
     (void)hipStreamDestroy(md->stream);
     delete md;
@@ -602,7 +732,7 @@ int smk_llama_reset(void* model, int capacity, const float* cos_table, const flo
     SMK_HIP(hipStreamSynchronize(md->stream), "reset");
     md->pos = 0;
     if (!md->g_logits) {
-        SMK_HIP(allow_lds(attention_kernel, static_cast<size_t>(capacity) * 4), "attention LDS");
+        SMK_HIP(allow_lds(attention_kernel, attention_lds(capacity, md->cfg.head_dim)), "attention LDS");
         SMK_HIP(capture(*md, true, &md->g_logits), "capture step");
         SMK_HIP(capture(*md, false, &md->g_plain), "capture step (no logits)");
     }
@@ -625,6 +755,34 @@ int smk_llama_step(void* model, int token, float* logits) {
                                md->stream),
                 "logits download");
     SMK_HIP(hipStreamSynchronize(md->stream), "step");
+    ++md->pos;
+    return ok();
+}
+
+int smk_llama_step_profile(void* model, int token, float* logits, double* section_ms, int n_sections) {
+    if (!model || !section_ms) return fail(SMK_ERR_ARGUMENT, "null argument");
+    auto* md = static_cast<Model*>(model);
+    if (n_sections < kSections) return fail(SMK_ERR_ARGUMENT, "section_ms needs " + std::to_string(kSections) + " entries");
+    if (!md->capacity) return fail(SMK_ERR_ARGUMENT, "call smk_llama_reset first");
+    if (md->pos >= md->capacity)
+        return fail(SMK_ERR_ARGUMENT, "KV cache full (" + std::to_string(md->capacity) + " positions)");
+    if (token < 0 || token >= md->cfg.vocab) return fail(SMK_ERR_ARGUMENT, "token out of range");
+    if (const int rc = use_device()) return rc;
+    md->host_pinned[2] = token;
+    SMK_HIP(hipMemcpyAsync(md->tokens + md->pos, md->host_pinned + 2, 4, hipMemcpyHostToDevice, md->stream), "token");
+    md->marks.id.clear();
+    SMK_HIP(enqueue_step(*md, logits != nullptr, &md->marks), "profiled step");
+    SMK_HIP(md->marks.mark(md->stream, kSections), "end mark");
+    if (logits)
+        SMK_HIP(hipMemcpyAsync(logits, md->logits, static_cast<size_t>(md->cfg.vocab) * 4, hipMemcpyDeviceToHost,
+                               md->stream),
+                "logits download");
+    SMK_HIP(hipStreamSynchronize(md->stream), "step");
+    for (size_t i = 0; i + 1 < md->marks.id.size(); ++i) {
+        float ms = 0.0f;
+        SMK_HIP(hipEventElapsedTime(&ms, md->marks.ev[i], md->marks.ev[i + 1]), "elapsed");
+        section_ms[md->marks.id[i]] += ms;
+    }
     ++md->pos;
     return ok();
 }

@@ -31,6 +31,7 @@
 // Lanes j, j+1, ... read consecutive 16-byte entries of a plane: no bank conflicts.
 #include "device_common.hpp"
 #include "launch.hpp"
+#include "pairwise_sum.hpp"
 
 #include <algorithm>
 
@@ -384,11 +385,16 @@ __device__ __forceinline__ void wave_lds_sync() {
 // N even (an odd N's last row goes to the generic kernel, which keeps q4_row_single's order).
 // CH: pairs one lane takes per row (K/64 <= CH * LPR).  The weights of the next group of rows
 // (CH pairs per lane) are loaded while the current group's two phases run.
+// norm_w != nullptr (M == 1, K <= 8192): x is first replaced by numpy's RMSNorm of it,
+// w * (x * float(1 / sqrt(mean(x*x) + eps))) (llama.py:184-187, the pairwise mean of squares
+// as the RMSNorm kernel computes it; norm_depth is the depth of its uniform tree), bit for bit
+// what the separate kernel would hand over.
 template <int LPR, int MT, int NT, int CH>
 __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K, const float* __restrict__ x,
                                                              int ldx, const uint8_t* __restrict__ W,
                                                              float* __restrict__ y, int ldy, int rows_per_wg,
-                                                             int accumulate) {
+                                                             int accumulate, const float* __restrict__ norm_w,
+                                                             double norm_eps, int norm_depth) {
     constexpr int D = 9;
     constexpr int G = kWave / LPR;           // rows side by side in one wave
     constexpr int kWaves = NT / kWave;
@@ -397,6 +403,7 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
     static_assert(4 * G * MT <= kWave, "phase 2 needs four lanes of the wave per row and row of x");
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ int bad[MT];
+    __shared__ float wave_sum[NT / kWave];
 
     const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
     const int S = ordered_stride(nb);
@@ -428,15 +435,53 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
         }
     };
 
-    XPreload<NT, PQ> xp;
-    xp.load(x, ldx, M, K);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_sched_barrier(0);
     uint32_t wa[CH][D], wb[CH][D];
-    load_group(0, wa);
-    __builtin_amdgcn_sched_barrier(0);
-    xp.template quantize<true, false>(x, ldx, M, K, lds_q, nullptr, lds_dx, bad);
-    lds_barrier();
+    if (norm_w) {
+        // x and the norm weights first (at most 4 quads a thread: K <= 16 * NT), then the first
+        // weights, so that waiting for x does not wait for W.
+        float* xf = scl + M * kRows * S;  // K floats
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        const float4* w4 = reinterpret_cast<const float4*>(norm_w);
+        float4 xr[4], wr[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int qd = static_cast<int>(threadIdx.x) + u * NT;
+            const int c = qd < quads ? qd : 0;
+            xr[u] = x4[c];
+            wr[u] = w4[c];
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_sched_barrier(0);
+        load_group(0, wa);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int qd = static_cast<int>(threadIdx.x) + u * NT;
+            if (qd < quads) reinterpret_cast<float4*>(xf)[qd] = xr[u];
+        }
+        lds_barrier();
+        const float total = uniform_chunk_sum<NT>(xf, K, norm_depth, wave_sum);
+        const float var = static_cast<float>(static_cast<double>(total) / static_cast<double>(K));
+        const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(var) + norm_eps));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int qd = static_cast<int>(threadIdx.x) + u * NT;
+            const bool live = qd < quads;
+            const float h[4] = {wr[u].x * (xr[u].x * scale), wr[u].y * (xr[u].y * scale),
+                                wr[u].z * (xr[u].z * scale), wr[u].w * (xr[u].w * scale)};
+            quantize_quad<true, false>(h, 0, live ? qd : 0, K, lds_q, nullptr, lds_dx, bad, live);
+        }
+        lds_barrier();
+    } else {
+        XPreload<NT, PQ> xp;
+        xp.load(x, ldx, M, K);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_sched_barrier(0);
+        load_group(0, wa);
+        __builtin_amdgcn_sched_barrier(0);
+        xp.template quantize<true, false>(x, ldx, M, K, lds_q, nullptr, lds_dx, bad);
+        lds_barrier();
+    }
 
     // Phase 1 of one pair: the four reference lanes' dots of both blocks, and the scales.
     auto phase1 = [&](int p, const uint32_t (&w)[D]) {
@@ -776,39 +821,46 @@ size_t ordered_lds_bytes(int M, int K, int rows_per_group) {
     return 4 * x_words + static_cast<size_t>(M) * rows_per_group * ordered_stride(static_cast<int>(nb)) * 20;
 }
 
+struct NormArgs {
+    const float* w = nullptr;
+    double eps = 0.0;
+    int depth = -1;
+};
+
 template <int LPR, int MT, int NT, int CH>
 hipError_t launch_ordered_ch(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
-                             int rows_per_wg, int acc, hipStream_t stream) {
+                             int rows_per_wg, int acc, const NormArgs& nrm, hipStream_t stream) {
     constexpr int kRows = NT / LPR;
-    const size_t lds = ordered_lds_bytes(M, K, kRows);
+    if (nrm.w && (M != 1 || (8 << nrm.depth) > NT)) return hipErrorInvalidValue;
+    const size_t lds = ordered_lds_bytes(M, K, kRows) + (nrm.w ? static_cast<size_t>(K) * 4 : 0);
     if (rows_per_wg <= 0) rows_per_wg = std::max(kRows, (N + 511) / 512);
     const int grid = (N + rows_per_wg - 1) / rows_per_wg;
     if (const hipError_t e = allow_lds(gemv_q4_ordered_kernel<LPR, MT, NT, CH>, lds); e != hipSuccess) return e;
     hipLaunchKernelGGL((gemv_q4_ordered_kernel<LPR, MT, NT, CH>), dim3(grid), dim3(NT), lds, stream, M, N, K, x, ldx,
-                       W, y, ldy, rows_per_wg, acc);
+                       W, y, ldy, rows_per_wg, acc, nrm.w, nrm.eps, nrm.depth);
     return hipGetLastError();
 }
 
 // Pairs per lane and row: 1, 2, 4 or 8 (the lane split is raised until that suffices).
 template <int LPR, int MT, int NT>
 hipError_t launch_ordered(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
-                          int rows_per_wg, int acc, hipStream_t stream) {
+                          int rows_per_wg, int acc, hipStream_t stream, const NormArgs& nrm = NormArgs()) {
     const int chunks = ((K >> 6) + LPR - 1) / LPR;
-    if (chunks <= 1) return launch_ordered_ch<LPR, MT, NT, 1>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, stream);
-    if (chunks <= 2) return launch_ordered_ch<LPR, MT, NT, 2>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, stream);
-    if (chunks <= 4) return launch_ordered_ch<LPR, MT, NT, 4>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, stream);
-    if (chunks <= 8) return launch_ordered_ch<LPR, MT, NT, 8>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, stream);
+    if (chunks <= 1) return launch_ordered_ch<LPR, MT, NT, 1>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
+    if (chunks <= 2) return launch_ordered_ch<LPR, MT, NT, 2>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
+    if (chunks <= 4) return launch_ordered_ch<LPR, MT, NT, 4>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
+    if (chunks <= 8) return launch_ordered_ch<LPR, MT, NT, 8>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
     return hipErrorInvalidValue;
 }
 
 template <int MT, int NT>
 hipError_t launch_ordered_lpr(int lpr, int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y,
-                              int ldy, int rows_per_wg, int acc, hipStream_t s) {
+                              int ldy, int rows_per_wg, int acc, hipStream_t s, const NormArgs& nrm = NormArgs()) {
     switch (lpr) {
-        case 64: return launch_ordered<64, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, s);
-        case 32: return launch_ordered<32, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, s);
-        case 16: return launch_ordered<16, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, s);
-        default: return launch_ordered<8, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, s);
+        case 64: return launch_ordered<64, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, s, nrm);
+        case 32: return launch_ordered<32, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, s, nrm);
+        case 16: return launch_ordered<16, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, s, nrm);
+        default: return launch_ordered<8, MT, NT>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, s, nrm);
     }
 }
 
@@ -830,6 +882,16 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
     const int pairs = (K >> 5) / 2;
     constexpr size_t kLdsCap = 150 * 1024;
     const bool generic = !pair_path_ok(K, W) || ordered_lds_bytes(M, K, 256 / 64) > kLdsCap || pairs > 8 * 64;
+    NormArgs nrm;
+    if (t && t->norm_w) {
+        // Fused RMSNorm: one row of x, K <= 8192, the pair kernel (even N), a uniform tree.
+        nrm.w = t->norm_w;
+        nrm.eps = t->norm_eps;
+        nrm.depth = uniform_depth(K);
+        if (M != 1 || K > 8192 || nrm.depth < 0 || generic || (N & 1) || (8 << nrm.depth) > 1024 ||
+            reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(t->norm_w) % 16)
+            return hipErrorInvalidValue;
+    }
     if (!generic && (N & 1)) {
         // The last row of an odd N has its own order (q4_row_single): one row through the
         // generic kernel, the even rest through the pair kernel.
@@ -862,15 +924,18 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
         const int per_cu = bytes < 24e6 ? 1 : (bytes < 128e6 ? 2 : 4);
         if (rpw <= 0) rpw = std::max(1, (N + g_cus * per_cu - 1) / (g_cus * per_cu));
         int nt = (t && t->threads) ? t->threads : ((bytes < 24e6 || bytes >= 128e6) ? 1024 : 512);
+        const size_t cap = kLdsCap - (nrm.w ? static_cast<size_t>(K) * 4 : 0);
         if (!(t && t->threads)) {
             while (nt > 256 && nt > rpw * lpr) nt /= 2;
-            while (nt > 256 && ordered_lds_bytes(1, K, nt / lpr) > kLdsCap) nt /= 2;
+            while (nt > 256 && ordered_lds_bytes(1, K, nt / lpr) > cap) nt /= 2;
         }
-        while (ordered_lds_bytes(1, K, nt / lpr) > kLdsCap && lpr < 64) lpr *= 2;
+        while (ordered_lds_bytes(1, K, nt / lpr) > cap && lpr < 64) lpr *= 2;
+        if (nrm.w)  // eight lanes per leaf of the norm's tree, at most four quads of x per thread
+            while (nt < (8 << nrm.depth) || nt * 16 < K) nt *= 2;
         switch (nt) {
-            case 1024: return launch_ordered_lpr<1, 1024>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
-            case 512: return launch_ordered_lpr<1, 512>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
-            default: return launch_ordered_lpr<1, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
+            case 1024: return launch_ordered_lpr<1, 1024>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream, nrm);
+            case 512: return launch_ordered_lpr<1, 512>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream, nrm);
+            default: return launch_ordered_lpr<1, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream, nrm);
         }
     }
     // Several rows of x: 256 threads, 32 or 64 lanes per row (phase 2 needs 4 * rows * M lanes).

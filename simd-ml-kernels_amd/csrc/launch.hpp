@@ -21,6 +21,8 @@ struct GemvTuning {
     int accumulate = 0;     // 1: y = y + x.W^T (one float32 add per output: a residual update)
     int unordered = 0;      // Q4_0 only, diagnostics: the free-order pair kernel instead of the
                             // reference's SIMD summation order
+    const float* norm_w = nullptr;  // Q4_0, one row of x: use RMSNorm(x) * norm_w instead of x
+    double norm_eps = 0.0;          // (numpy-exact, as rms_norm), K <= 8192, N even
 };
 
 // y[m*ldy + n] = sum_k x[m*ldx + k] * W[n][k] for m < M (M <= 8), W in GGUF Q4_0 (block_bytes 18)

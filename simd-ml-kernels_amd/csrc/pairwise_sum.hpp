@@ -1,0 +1,86 @@
+// pairwise_sum.hpp -- numpy's float32 pairwise summation on a workgroup (RMSNorm's mean of
+// squares), shared by the RMSNorm kernels and the GEMV prologue that normalizes x itself.
+#pragma once
+
+#include "device_common.hpp"
+
+namespace smk {
+
+// Fast path for chunks whose pairwise tree has every leaf at one depth D (all common model
+// widths: 2048 = 16 leaves of 128, 8192 = 64 of 128, and the last chunk of 14336 = 6144 =
+// 64 leaves of 96).  Leaf l (0 <= l < 2^D) is reached by following the bits of l from the
+// root, left on 0.  Eight lanes per leaf hold numpy's eight interleaved accumulators,
+// combined as ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) (DPP; a+b == b+a bit for bit), then the
+// leaf's last len % 8 values are added in order.  Sibling subtrees are then added level by
+// level: within a wave by lane exchange, across waves through LDS in the same pairing.
+__device__ __forceinline__ void leaf_of(int l, int depth, int n, int& start, int& len) {
+    start = 0;
+    len = n;
+    for (int d = depth - 1; d >= 0; --d) {
+        int n2 = len / 2;
+        n2 -= n2 % 8;
+        if ((l >> d) & 1) {
+            start += n2;
+            len -= n2;
+        } else {
+            len = n2;
+        }
+    }
+}
+
+template <int kThreads>
+__device__ __forceinline__ float uniform_chunk_sum(const float* __restrict__ q, int n, int depth, float* wave_sum) {
+    constexpr int kWaves = kThreads / kWave;
+    const int leaves = 1 << depth;
+    const int l = threadIdx.x >> 3, k = threadIdx.x & 7;
+    float r = 0.0f;
+    int start = 0, len = 0;
+    if (l < leaves) {
+        leaf_of(l, depth, n, start, len);
+        const int full = len - (len % 8);
+        float v = q[start + k];
+        r = v * v;
+        for (int i = 8 + k; i < full; i += 8) {
+            v = q[start + i];
+            r = r + v * v;
+        }
+    }
+    r = r + dpp_f<kDppQuadXor1>(r);
+    r = r + dpp_f<kDppQuadXor2>(r);
+    r = r + dpp_f<kDppHalfMirror>(r);
+    if (l < leaves) {
+        for (int i = len - (len % 8); i < len; ++i) {
+            const float v = q[start + i];
+            r = r + v * v;
+        }
+    }
+    // Sibling leaves: lanes xor 8, 16, 32 hold leaves l^1, l^2, l^4 of the same wave.
+    for (int lv = 0; lv < 3 && (2 << lv) <= leaves; ++lv) r = r + __shfl_xor(r, 8 << lv, kWave);
+    if ((threadIdx.x & (kWave - 1)) == 0) wave_sum[threadIdx.x / kWave] = r;
+    __syncthreads();
+    const int used = leaves >= 8 ? leaves / 8 : 1;  // waves that hold leaves
+    float v[kWaves];
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) v[i] = wave_sum[i];
+#pragma unroll
+    for (int width = 1; width < kWaves; width *= 2)
+#pragma unroll
+        for (int i = 0; i + width < kWaves; i += 2 * width)
+            if (i + width < used) v[i] = v[i] + v[i + width];
+    __syncthreads();  // wave_sum is rewritten by the next chunk
+    return v[0];
+}
+
+
+// Depth at which every leaf of numpy's pairwise tree over len values sits, or -1 when the
+// leaves sit at different depths (or len < 8, where numpy sums sequentially).
+inline int uniform_depth(int len) {
+    if (len < 8) return -1;
+    if (len <= 128) return 0;
+    int n2 = len / 2;
+    n2 -= n2 % 8;
+    const int a = uniform_depth(n2), b = uniform_depth(len - n2);
+    return (a >= 0 && a == b) ? a + 1 : -1;
+}
+
+}  // namespace smk

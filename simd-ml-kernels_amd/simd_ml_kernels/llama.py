@@ -274,7 +274,9 @@ class Llama:
             raise RuntimeError("call reset() first")
         if self.pos >= self.capacity:
             raise ValueError(f"KV cache full ({self.capacity} positions)")
-        if self._engine is not None:
+        if self._engine is not None and self.profile is not None:
+            out = self._engine.step_profile(int(token), logits, self.profile)
+        elif self._engine is not None:
             out = self._engine.step(int(token), logits)
         elif self.profile is not None:
             out = self._host_step(int(token), logits, self.profile)
@@ -443,6 +445,29 @@ class _Engine:
     def step(self, token: int, logits: bool) -> np.ndarray | None:
         out = np.empty(self.cfg.vocab_size, np.float32) if logits else None
         abi.check(self.L.smk_llama_step(self.h, token, out.ctypes.data if logits else None), "smk_llama_step")
+        return out
+
+    DEVICE_SECTIONS = ("embed", "rms_norm", "gemv_qkv", "rope_kv", "attention", "gemv_o", "gemv_gate_up",
+                       "silu_mul", "gemv_down", "lm_head", "argmax")
+    # The example's profile sections (llama.py:441-479) from the device sections.
+    _GROUPS = {"gemv": ("gemv_qkv", "gemv_o", "gemv_gate_up", "gemv_down", "lm_head"), "attention": ("attention",),
+               "norm_rope_silu": ("rms_norm", "rope_kv", "silu_mul")}
+
+    def step_profile(self, token: int, logits: bool, prof: dict) -> np.ndarray | None:
+        """One eager step with a HIP event per section; seconds summed into prof like the example's
+        profile dict (gemv, attention, norm_rope_silu, total, steps), device sections in
+        prof["device"]."""
+        out = np.empty(self.cfg.vocab_size, np.float32) if logits else None
+        ms = np.zeros(len(self.DEVICE_SECTIONS), np.float64)
+        abi.check(self.L.smk_llama_step_profile(self.h, token, out.ctypes.data if logits else None, ms.ctypes.data,
+                                                len(ms)), "smk_llama_step_profile")
+        dev = prof.setdefault("device", {})
+        for name, v in zip(self.DEVICE_SECTIONS, ms):
+            dev[name] = dev.get(name, 0.0) + v * 1e-3
+        for grp, names in self._GROUPS.items():
+            prof[grp] = prof.get(grp, 0.0) + sum(ms[self.DEVICE_SECTIONS.index(n)] for n in names) * 1e-3
+        prof["total"] = prof.get("total", 0.0) + float(ms.sum()) * 1e-3
+        prof["steps"] = prof.get("steps", 0) + 1
         return out
 
     def generate(self, prompt: list[int], n_new: int) -> tuple[np.ndarray, float, float]:
