@@ -3,12 +3,12 @@
 // weight, activation and the KV cache in HBM, and one HIP graph per token.
 //
 // Per layer, the step runs (llama.py:428-434):
-//   h = rms_norm(x, attn_norm)                   rms_norm kernel (numpy-exact)
+//   h = rms_norm(x, attn_norm)                   in the GEMV's prologue (numpy-exact; Q4_0),
 //   [q|k|v] = h @ [Wq;Wk;Wv]^T                   one GEMV over the three matrices' rows
-//   q, k = rope(q), rope(k); cache[pos] = k, v   rope_kv_kernel
+//   q, k = rope(q), rope(k); cache[pos] = k, v   in attention_kernel
 //   a = attention(q, cache[0..pos])              attention_kernel (one workgroup per head)
 //   x = x + a @ Wo^T                             GEMV with a residual epilogue
-//   h = rms_norm(x, mlp_norm)
+//   h = rms_norm(x, mlp_norm)                    in the GEMV's prologue
 //   [g|u] = h @ [Wgate;Wup]^T                    one GEMV
 //   x = x + (silu(g) * u) @ Wdown^T              silu_mul_kernel, GEMV with residual epilogue
 // then logits = rms_norm(x, norm) @ lm_head^T and the greedy argmax on the device.
@@ -73,47 +73,12 @@ __global__ void embed_kernel(const uint8_t* __restrict__ E, int type, int hidden
     }
 }
 
-// RoPE of q (in place) and k, and the cache write of k and v at st->pos.  qkv holds n_heads q
-// heads, then n_kv k heads, then n_kv v heads.  Caches: [n_kv, cap, hd] of this layer.
-__global__ void rope_kv_kernel(float* __restrict__ qkv, const float* __restrict__ cos_tab,
-                               const float* __restrict__ sin_tab, int n_heads, int n_kv, int hd, int interleaved,
-                               float* __restrict__ kc, float* __restrict__ vc, int cap,
-                               const DecodeState* __restrict__ st) {
-    const int pos = st->pos;
-    const float* cs = cos_tab + static_cast<size_t>(pos) * hd;
-    const float* sn = sin_tab + static_cast<size_t>(pos) * hd;
-    const int half = hd / 2;
-    const int rot = (n_heads + n_kv) * half;
-    const int total = rot + n_kv * hd;
-    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < total; t += gridDim.x * blockDim.x) {
-        if (t < rot) {
-            const int head = t / half, i = t - head * half;
-            const float* xr = qkv + static_cast<size_t>(head) * hd;
-            float* dst = head < n_heads ? qkv + static_cast<size_t>(head) * hd
-                                        : kc + (static_cast<size_t>(head - n_heads) * cap + pos) * hd;
-            if (interleaved) {
-                const float a = xr[2 * i], b = xr[2 * i + 1];
-                float o0, o1;
-                rope_pair_interleaved(a, b, cs[i], sn[i], o0, o1);
-                dst[2 * i] = o0;
-                dst[2 * i + 1] = o1;
-            } else {
-                const float lo = xr[i], hi = xr[half + i];
-                float o0, o1;
-                rope_pair_half(lo, hi, cs[i], sn[i], cs[half + i], sn[half + i], o0, o1);
-                dst[i] = o0;
-                dst[half + i] = o1;
-            }
-        } else {
-            const int u = t - rot, g = u / hd, d = u - g * hd;
-            vc[(static_cast<size_t>(g) * cap + pos) * hd + d] = qkv[static_cast<size_t>(n_heads + n_kv) * hd + u];
-        }
-    }
-}
-
-// Grouped-query attention of one query head over positions 0..pos (llama.py:398-412), in the
-// arithmetic order of the reference's SIMD tables, so that every score, probability and output
-// equals the reference's bit for bit:
+// Grouped-query attention of one query head over positions 0..pos (llama.py:398-412) with the
+// RoPE of the step folded in, in the arithmetic order of the reference's SIMD tables, so that
+// every score, probability and output equals the reference's bit for bit:
+//   q, k = rope(q), rope(k) (llama.py:387-396 interleaved, :169-178 half split; numpy's
+//     separate roundings); the first workgroup of each KV group writes k and v into the cache at
+//     pos, and every workgroup uses its own copies for position pos (same values);
 //   scores = sk.sgemm(q, K, alpha=scale, trans_b=True): the AVX-512 few-row dot
 //     (avx512_gemm_packed.cpp:216-240): 16 lanes per dot, lane l accumulating products
 //     p = l, l+32, ... and 16+l, 48+l, ... in two fused chains, the two chains added, the 16
@@ -122,64 +87,142 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, const float* __restrict_
 //     of 8, eight running double sums, a double exp on the last n % 8);
 //   out = sk.sgemm(p, V): the AVX2 direct product (avx2_gemm_packed.cpp:151-201), one fused
 //     chain over the positions in order per output.
-// One workgroup of 256 threads per head; scores in LDS; K and V read in tiles of kTile
-// positions staged through LDS with coalesced loads.
+// One workgroup of 256 threads per query head; scores in LDS; cached K and V read in tiles of
+// kTile positions staged through LDS (the K and V tiles of a round are loaded together).
 constexpr int kAttnThreads = 256;
-constexpr int kTile = 64;
+constexpr int kTile = 128;
 
 // count floats (a multiple of 4, 16-byte aligned ends) from global to LDS: every thread issues
-// its four 16-byte loads of a round before storing any (no load waits for an earlier store).
-__device__ __forceinline__ void stage_tile(float* __restrict__ dst, const float* __restrict__ src, int count) {
-    const float4* s4 = reinterpret_cast<const float4*>(src);
-    float4* d4 = reinterpret_cast<float4*>(dst);
+// its 16-byte loads of a round before storing any (no load waits for an earlier store).
+__device__ __forceinline__ void stage_tiles(float* __restrict__ d0, const float* __restrict__ s0,
+                                            float* __restrict__ d1, const float* __restrict__ s1, int count) {
+    const float4* a4 = reinterpret_cast<const float4*>(s0);
+    const float4* b4 = reinterpret_cast<const float4*>(s1);
     const int n4 = count >> 2;
     for (int base = 0; base < n4; base += 4 * kAttnThreads) {
-        float4 v[4];
+        float4 va[4], vb[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int e = base + u * kAttnThreads + static_cast<int>(threadIdx.x);
-            v[u] = s4[e < n4 ? e : 0];
+            va[u] = a4[e < n4 ? e : 0];
+            if (d1) vb[u] = b4[e < n4 ? e : 0];
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int e = base + u * kAttnThreads + static_cast<int>(threadIdx.x);
-            if (e < n4) d4[e] = v[u];
+            if (e < n4) {
+                reinterpret_cast<float4*>(d0)[e] = va[u];
+                if (d1) reinterpret_cast<float4*>(d1)[e] = vb[u];
+            }
         }
     }
 }
 
-__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __restrict__ q_all,
-                                                                 const float* __restrict__ kc,
-                                                                 const float* __restrict__ vc, int n_heads, int n_kv,
-                                                                 int hd, int cap, float scale,
+// RoPE of one head of hd values in place in LDS (hd / 2 threads).
+__device__ __forceinline__ void rope_head_lds(float* v, const float* cs, const float* sn, int hd, int interleaved) {
+    const int half = hd / 2, i = threadIdx.x;
+    if (i < half) {
+        if (interleaved) {
+            float o0, o1;
+            rope_pair_interleaved(v[2 * i], v[2 * i + 1], cs[i], sn[i], o0, o1);
+            v[2 * i] = o0;
+            v[2 * i + 1] = o1;
+        } else {
+            float o0, o1;
+            rope_pair_half(v[i], v[half + i], cs[i], sn[i], cs[half + i], sn[half + i], o0, o1);
+            v[i] = o0;
+            v[half + i] = o1;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __restrict__ qkv,
+                                                                 const float* __restrict__ cos_tab,
+                                                                 const float* __restrict__ sin_tab, int interleaved,
+                                                                 float* __restrict__ kc, float* __restrict__ vc,
+                                                                 int n_heads, int n_kv, int hd, int cap, float scale,
                                                                  const DecodeState* __restrict__ st,
                                                                  float* __restrict__ out) {
-    extern __shared__ float sc[];  // T scores, then probabilities; then the K / V tile
-    __shared__ float qs[256];
+    extern __shared__ float sc[];  // T scores then probabilities; then the K and V tiles
+    __shared__ float qs[256], ks[256], vs[256];
     __shared__ float red_f[kAttnThreads / kWave];
     __shared__ int red_i[kAttnThreads / kWave];
     __shared__ double lane_sum[8];
     __shared__ double tail_e[8];
     __shared__ float inv_s;
     const int head = blockIdx.x;
-    const int g = head / (n_heads / n_kv);
-    const int T = st->pos + 1;
+    const int rep = n_heads / n_kv, g = head / rep;
+    const int pos = st->pos, T = pos + 1;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     constexpr int kWaves = kAttnThreads / kWave;
-    float* tile = sc + ((cap + 3) & ~3);  // kTile * hd floats
-    for (int d = threadIdx.x; d < hd; d += kAttnThreads) qs[d] = q_all[static_cast<size_t>(head) * hd + d];
-    const float* K = kc + static_cast<size_t>(g) * cap * hd;
-    const float* V = vc + static_cast<size_t>(g) * cap * hd;
-    // Scores, a tile of positions at a time: 16 lanes per position.
+    float* ktile = sc + ((cap + 3) & ~3);   // kTile * hd
+    float* vtile = ktile + kTile * hd;      // kTile * hd
+    float* K = kc + static_cast<size_t>(g) * cap * hd;
+    float* V = vc + static_cast<size_t>(g) * cap * hd;
+    // This step's q, k, v and the first round's cached K and V (positions < pos), all loads
+    // issued before any store.
+    const int first_cached = min(min(kTile, T), pos);
+    {
+        const int d = threadIdx.x;
+        float q0 = 0.0f, k0 = 0.0f, v0 = 0.0f;
+        if (d < hd) {
+            q0 = qkv[static_cast<size_t>(head) * hd + d];
+            k0 = qkv[static_cast<size_t>(n_heads + g) * hd + d];
+            v0 = qkv[static_cast<size_t>(n_heads + n_kv + g) * hd + d];
+        }
+        const int n4 = first_cached * hd / 4;
+        constexpr int kPer = 8;  // float4 per thread of one tile (kTile * 64 / 4 / 256); more rounds if larger
+        float4 ka[kPer], va[kPer];
+        const float4* k4 = reinterpret_cast<const float4*>(K);
+        const float4* v4 = reinterpret_cast<const float4*>(V);
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int e = u * kAttnThreads + static_cast<int>(threadIdx.x);
+            ka[u] = k4[e < n4 ? e : 0];
+            va[u] = v4[e < n4 ? e : 0];
+        }
+        if (d < hd) {
+            qs[d] = q0;
+            ks[d] = k0;
+            vs[d] = v0;
+        }
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int e = u * kAttnThreads + static_cast<int>(threadIdx.x);
+            if (e < n4) {
+                reinterpret_cast<float4*>(ktile)[e] = ka[u];
+                reinterpret_cast<float4*>(vtile)[e] = va[u];
+            }
+        }
+        for (int e = kPer * kAttnThreads + static_cast<int>(threadIdx.x); e < n4; e += kAttnThreads) {
+            reinterpret_cast<float4*>(ktile)[e] = k4[e];  // head_dim > 64
+            reinterpret_cast<float4*>(vtile)[e] = v4[e];
+        }
+    }
+    __syncthreads();
+    const float* cs = cos_tab + static_cast<size_t>(pos) * hd;
+    const float* sn = sin_tab + static_cast<size_t>(pos) * hd;
+    rope_head_lds(qs, cs, sn, hd, interleaved);
+    rope_head_lds(ks, cs, sn, hd, interleaved);
+    __syncthreads();
+    if (head % rep == 0)
+        for (int d = threadIdx.x; d < hd; d += kAttnThreads) {
+            K[static_cast<size_t>(pos) * hd + d] = ks[d];
+            V[static_cast<size_t>(pos) * hd + d] = vs[d];
+        }
+    // Scores and the V tiles, kTile positions a round.  Position pos comes from ks / vs.
     const int l = threadIdx.x & 15;
     for (int t0 = 0; t0 < T; t0 += kTile) {
         const int tn = min(kTile, T - t0);
-        __syncthreads();  // the previous tile is consumed (and qs is written, first time)
-        stage_tile(tile, K + static_cast<size_t>(t0) * hd, tn * hd);
+        const int cached = min(tn, pos - t0);  // positions of this round read from the cache
+        __syncthreads();  // the previous round's tiles are consumed
+        if (cached > 0 && t0 > 0) stage_tiles(ktile, K + static_cast<size_t>(t0) * hd, nullptr, nullptr, cached * hd);
+        if (cached < tn)
+            for (int d = threadIdx.x; d < hd; d += kAttnThreads) ktile[(pos - t0) * hd + d] = ks[d];
         __syncthreads();
         for (int tt = threadIdx.x >> 4; tt < kTile; tt += kAttnThreads / 16) {
             const int tc = min(tt, tn - 1);
-            const float* kr = tile + tc * hd;
+            const float* kr = ktile + tc * hd;
             float a0 = 0.0f, a1 = 0.0f;
             for (int p = 0; p < hd; p += 32) {
                 if (p + l < hd) a0 = fmaf(qs[p + l], kr[p + l], a0);
@@ -244,21 +287,26 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     __syncthreads();
     const float inv = inv_s;
     for (int t = threadIdx.x; t < T; t += kAttnThreads) sc[t] = nan_row ? __builtin_nanf("") : sc[t] * inv;
-    // out[d] = one fused chain over the positions in order, V staged a tile at a time.
+    // out[d] = one fused chain over the positions in order.
     float acc = 0.0f;
     const int d = threadIdx.x;
     for (int t0 = 0; t0 < T; t0 += kTile) {
         const int tn = min(kTile, T - t0);
+        const int cached = min(tn, pos - t0);
         __syncthreads();  // probabilities written / the previous tile consumed
-        stage_tile(tile, V + static_cast<size_t>(t0) * hd, tn * hd);
+        if (cached > 0 && t0 > 0) stage_tiles(vtile, V + static_cast<size_t>(t0) * hd, nullptr, nullptr, cached * hd);
+        if (cached < tn)
+            for (int e = threadIdx.x; e < hd; e += kAttnThreads) vtile[(pos - t0) * hd + e] = vs[e];
         __syncthreads();
-        if (d < hd)
-            for (int t = 0; t < tn; ++t) acc = fmaf(sc[t0 + t], tile[t * hd + d], acc);
+        if (d < hd) {
+#pragma unroll 8
+            for (int t = 0; t < tn; ++t) acc = fmaf(sc[t0 + t], vtile[t * hd + d], acc);
+        }
     }
     if (d < hd) out[static_cast<size_t>(head) * hd + d] = acc;
 }
 
-size_t attention_lds(int cap, int hd) { return (static_cast<size_t>((cap + 3) & ~3) + static_cast<size_t>(kTile) * hd) * 4; }
+size_t attention_lds(int cap, int hd) { return (static_cast<size_t>((cap + 3) & ~3) + 2 * static_cast<size_t>(kTile) * hd) * 4; }
 
 // m = silu(g) * u (llama.py:434: sk.silu(gate) * up, two float32 results multiplied), SiLU as
 // the reference's SIMD tables compute it.
@@ -413,6 +461,7 @@ struct Model {
     hipGraphExec_t g_logits = nullptr, g_plain = nullptr;
     std::vector<unsigned> loaded;  // bit per tensor per layer
     bool fuse_norm = false;        // Q4_0 GEMVs normalize x themselves
+    bool fuse_silu = false;        // gate/up rows interleaved; the GEMV writes silu(gate) * up
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     Marks marks;
     uint64_t weight_bytes = 0;
@@ -445,15 +494,17 @@ void free_capacity(Model& md) {
 hipError_t gemv(const Mat& W, const float* x, float* y, bool accumulate, hipStream_t s);
 
 hipError_t gemv_normed(const Model& md, const Mat& W, const float* x, const float* nw, float* h, float* y,
-                       bool accumulate) {
+                       bool accumulate, bool silu_pairs = false) {
+    GemvTuning t;
+    t.accumulate = accumulate ? 1 : 0;
+    t.silu_pairs = silu_pairs ? 1 : 0;
     if (md.fuse_norm && W.type == kGgmlQ4_0) {
-        GemvTuning t;
-        t.accumulate = accumulate ? 1 : 0;
         t.norm_w = nw;
         t.norm_eps = md.cfg.rms_eps;
         return gemv_quant(kQ4_0Bytes, 1, W.rows, W.cols, x, W.cols, W.p, y, W.rows, md.stream, &t);
     }
     if (const hipError_t e = rms_norm(x, nw, h, 1, md.cfg.hidden, md.cfg.rms_eps, md.stream); e != hipSuccess) return e;
+    if (silu_pairs) return gemv_quant(kQ4_0Bytes, 1, W.rows, W.cols, h, W.cols, W.p, y, W.rows, md.stream, &t);
     return gemv(W, h, y, accumulate, md.stream);
 }
 
@@ -482,7 +533,6 @@ hipError_t enqueue_step(Model& md, bool with_logits, Marks* mk = nullptr) {
     if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     const size_t layer_kv = static_cast<size_t>(nkv) * md.capacity * hd;
     const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(hd)));
-    const int rope_total = (nh + nkv) * (hd / 2) + nkv * hd;
     for (int l = 0; l < c.n_layers; ++l) {
         const Layer& L = md.layers[l];
         float* kc = md.kc + l * layer_kv;
@@ -490,20 +540,22 @@ hipError_t enqueue_step(Model& md, bool with_logits, Marks* mk = nullptr) {
         SMK_MARK(kGemvQkv);
         hipError_t e = gemv_normed(md, L.qkv, md.x, L.attn_norm, md.h, md.qkv, false);
         if (e != hipSuccess) return e;
-        SMK_MARK(kRopeKv);
-        hipLaunchKernelGGL(rope_kv_kernel, dim3((rope_total + 255) / 256), dim3(256), 0, s, md.qkv, md.cos_tab,
-                           md.sin_tab, nh, nkv, hd, c.rope_interleaved, kc, vc, md.capacity, md.st);
         SMK_MARK(kAttention);
         hipLaunchKernelGGL(attention_kernel, dim3(nh), dim3(kAttnThreads), attention_lds(md.capacity, hd), s,
-                           md.qkv, kc, vc, nh, nkv, hd, md.capacity, scale, md.st, md.attn);
+                           md.qkv, md.cos_tab, md.sin_tab, c.rope_interleaved, kc, vc, nh, nkv, hd, md.capacity,
+                           scale, md.st, md.attn);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         SMK_MARK(kGemvO);
         if ((e = gemv(L.o, md.attn, md.x, true, s)) != hipSuccess) return e;
         SMK_MARK(kGemvGateUp);
-        if ((e = gemv_normed(md, L.gateup, md.x, L.ffn_norm, md.h, md.gu, false)) != hipSuccess) return e;
-        SMK_MARK(kSiluMul);
-        hipLaunchKernelGGL(silu_mul_kernel, dim3((c.ffn + 255) / 256), dim3(256), 0, s, md.gu, c.ffn, md.m);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (md.fuse_silu) {
+            if ((e = gemv_normed(md, L.gateup, md.x, L.ffn_norm, md.h, md.m, false, true)) != hipSuccess) return e;
+        } else {
+            if ((e = gemv_normed(md, L.gateup, md.x, L.ffn_norm, md.h, md.gu, false)) != hipSuccess) return e;
+            SMK_MARK(kSiluMul);
+            hipLaunchKernelGGL(silu_mul_kernel, dim3((c.ffn + 255) / 256), dim3(256), 0, s, md.gu, c.ffn, md.m);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
         SMK_MARK(kGemvDown);
         if ((e = gemv(L.down, md.m, md.x, true, s)) != hipSuccess) return e;
     }
@@ -632,8 +684,9 @@ int smk_llama_create(const smk_llama_config* cfg, void** model) {
     if (md->tied) md->head = md->embed;
     {
         const int depth = uniform_depth(c.hidden);
-        md->fuse_norm = c.hidden <= 8192 && c.hidden % 64 == 0 && depth >= 0 && (8 << depth) <= 1024 &&
-                        (md->q_rows() + 2 * md->kv_rows()) % 2 == 0 && c.ffn % 2 == 0 && c.vocab % 2 == 0;
+        md->fuse_norm = c.matrix_type == kGgmlQ4_0 && c.hidden <= 8192 && c.hidden % 64 == 0 && depth >= 0 &&
+                        (8 << depth) <= 1024 && (md->q_rows() + 2 * md->kv_rows()) % 2 == 0 && c.vocab % 2 == 0;
+        md->fuse_silu = c.matrix_type == kGgmlQ4_0 && c.hidden % 64 == 0;
     }
     md->weight_bytes = md->head.bytes();
     for (const Layer& L : md->layers) md->weight_bytes += L.qkv.bytes() + L.o.bytes() + L.gateup.bytes() + L.down.bytes();
@@ -687,8 +740,23 @@ int smk_llama_set_tensor(void* model, int tensor, int layer, const void* host, s
             case T_K: dst = L.qkv.p + static_cast<size_t>(qr) * L.qkv.row_bytes(); want = static_cast<size_t>(kr) * L.qkv.row_bytes(); break;
             case T_V: dst = L.qkv.p + static_cast<size_t>(qr + kr) * L.qkv.row_bytes(); want = static_cast<size_t>(kr) * L.qkv.row_bytes(); break;
             case T_O: dst = L.o.p; want = L.o.bytes(); break;
-            case T_GATE: dst = L.gateup.p; want = static_cast<size_t>(c.ffn) * L.gateup.row_bytes(); break;
-            case T_UP: dst = L.gateup.p + static_cast<size_t>(c.ffn) * L.gateup.row_bytes(); want = static_cast<size_t>(c.ffn) * L.gateup.row_bytes(); break;
+            case T_GATE:
+            case T_UP: {
+                // Gate rows then up rows; interleaved (gate_n, up_n) when the GEMV fuses the SiLU.
+                const size_t rb = L.gateup.row_bytes();
+                want = static_cast<size_t>(c.ffn) * rb;
+                if (nbytes != want) break;
+                if (md->fuse_silu) {
+                    SMK_HIP(hipMemcpy2D(L.gateup.p + (tensor == T_UP ? rb : 0), 2 * rb, host, rb, rb, c.ffn,
+                                        hipMemcpyHostToDevice),
+                            "tensor upload");
+                } else {
+                    SMK_HIP(hipMemcpy(L.gateup.p + (tensor == T_UP ? c.ffn * rb : 0), host, want, hipMemcpyHostToDevice),
+                            "tensor upload");
+                }
+                md->loaded[1 + layer] |= 1u << tensor;
+                return ok();
+            }
             case T_DOWN: dst = L.down.p; want = L.down.bytes(); break;
         }
     }

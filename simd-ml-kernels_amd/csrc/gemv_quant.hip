@@ -394,7 +394,7 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
                                                              int ldx, const uint8_t* __restrict__ W,
                                                              float* __restrict__ y, int ldy, int rows_per_wg,
                                                              int accumulate, const float* __restrict__ norm_w,
-                                                             double norm_eps, int norm_depth) {
+                                                             double norm_eps, int norm_depth, int silu_pairs) {
     constexpr int D = 9;
     constexpr int G = kWave / LPR;           // rows side by side in one wave
     constexpr int kWaves = NT / kWave;
@@ -546,7 +546,13 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
             }
             a = a + dpp_f<kDppQuadXor2>(a);   // lanes k and k + 2
             a = a + dpp_f<kDppQuadXor1>(a);   // then the two pair sums
-            if (k == 0 && row < row_end) {
+            if (silu_pairs) {
+                // Rows 2n and 2n + 1 are gate_n and up_n (G even, rows of a group aligned):
+                // y[n] = silu(gate_n) * up_n as the reference's SIMD SiLU, then one product.
+                const float up = __shfl_xor(a, 4, kWave);
+                if (k == 0 && (rg & 1) == 0 && row < row_end)
+                    y[static_cast<size_t>(m) * ldy + (row >> 1)] = bad[m] ? __builtin_nanf("") : silu_ref(a) * up;
+            } else if (k == 0 && row < row_end) {
                 float* yp = y + static_cast<size_t>(m) * ldy + row;
                 *yp = bad[m] ? __builtin_nanf("") : (accumulate ? *yp + a : a);
             }
@@ -815,6 +821,8 @@ hipError_t launch_generic(int M, int N, int K, const float* x, int ldx, const ui
 
 // ─── Q4_0 launchers (the reference's SIMD order) ─────────────────────────────
 
+inline bool accumulate_unsupported(int acc) { return acc != 0; }  // the SiLU-pair epilogue overwrites
+
 size_t ordered_lds_bytes(int M, int K, int rows_per_group) {
     const size_t nb = static_cast<size_t>(K) >> 5, quads = static_cast<size_t>(K) >> 2;
     const size_t x_words = (M * (quads + nb) + 3) & ~static_cast<size_t>(3);
@@ -825,6 +833,7 @@ struct NormArgs {
     const float* w = nullptr;
     double eps = 0.0;
     int depth = -1;
+    int silu_pairs = 0;  // epilogue: rows (2n, 2n+1) -> y[n] = silu(row 2n) * row 2n+1
 };
 
 template <int LPR, int MT, int NT, int CH>
@@ -832,12 +841,13 @@ hipError_t launch_ordered_ch(int M, int N, int K, const float* x, int ldx, const
                              int rows_per_wg, int acc, const NormArgs& nrm, hipStream_t stream) {
     constexpr int kRows = NT / LPR;
     if (nrm.w && (M != 1 || (8 << nrm.depth) > NT)) return hipErrorInvalidValue;
+    if (nrm.silu_pairs && (LPR > 32 || (rows_per_wg & 1) || accumulate_unsupported(acc))) return hipErrorInvalidValue;
     const size_t lds = ordered_lds_bytes(M, K, kRows) + (nrm.w ? static_cast<size_t>(K) * 4 : 0);
     if (rows_per_wg <= 0) rows_per_wg = std::max(kRows, (N + 511) / 512);
     const int grid = (N + rows_per_wg - 1) / rows_per_wg;
     if (const hipError_t e = allow_lds(gemv_q4_ordered_kernel<LPR, MT, NT, CH>, lds); e != hipSuccess) return e;
     hipLaunchKernelGGL((gemv_q4_ordered_kernel<LPR, MT, NT, CH>), dim3(grid), dim3(NT), lds, stream, M, N, K, x, ldx,
-                       W, y, ldy, rows_per_wg, acc, nrm.w, nrm.eps, nrm.depth);
+                       W, y, ldy, rows_per_wg, acc, nrm.w, nrm.eps, nrm.depth, nrm.silu_pairs);
     return hipGetLastError();
 }
 
@@ -883,6 +893,10 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
     constexpr size_t kLdsCap = 150 * 1024;
     const bool generic = !pair_path_ok(K, W) || ordered_lds_bytes(M, K, 256 / 64) > kLdsCap || pairs > 8 * 64;
     NormArgs nrm;
+    if (t && t->silu_pairs) {
+        if (M != 1 || generic || (N & 1)) return hipErrorInvalidValue;
+        nrm.silu_pairs = 1;
+    }
     if (t && t->norm_w) {
         // Fused RMSNorm: one row of x, K <= 8192, the pair kernel (even N), a uniform tree.
         nrm.w = t->norm_w;
@@ -923,13 +937,17 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
         const double bytes = static_cast<double>(N) * (K >> 5) * kQ4_0Bytes;
         const int per_cu = bytes < 24e6 ? 1 : (bytes < 128e6 ? 2 : 4);
         if (rpw <= 0) rpw = std::max(1, (N + g_cus * per_cu - 1) / (g_cus * per_cu));
+        if (nrm.silu_pairs) {
+            rpw += rpw & 1;            // (gate, up) pairs never straddle workgroups
+            if (lpr > 32) lpr = 32;    // and two rows at least side by side in a wave
+        }
         int nt = (t && t->threads) ? t->threads : ((bytes < 24e6 || bytes >= 128e6) ? 1024 : 512);
         const size_t cap = kLdsCap - (nrm.w ? static_cast<size_t>(K) * 4 : 0);
         if (!(t && t->threads)) {
             while (nt > 256 && nt > rpw * lpr) nt /= 2;
             while (nt > 256 && ordered_lds_bytes(1, K, nt / lpr) > cap) nt /= 2;
         }
-        while (ordered_lds_bytes(1, K, nt / lpr) > cap && lpr < 64) lpr *= 2;
+        while (ordered_lds_bytes(1, K, nt / lpr) > cap && lpr < (nrm.silu_pairs ? 32 : 64)) lpr *= 2;
         if (nrm.w)  // eight lanes per leaf of the norm's tree, at most four quads of x per thread
             while (nt < (8 << nrm.depth) || nt * 16 < K) nt *= 2;
         switch (nt) {

@@ -23,6 +23,8 @@ struct GemvTuning {
                             // reference's SIMD summation order
     const float* norm_w = nullptr;  // Q4_0, one row of x: use RMSNorm(x) * norm_w instead of x
     double norm_eps = 0.0;          // (numpy-exact, as rms_norm), K <= 8192, N even
+    int silu_pairs = 0;             // Q4_0, one row of x, N even: rows 2n, 2n+1 are (gate, up);
+                                    // y[n] = silu(gate) * up (y has N / 2 entries)
 };
 
 // y[m*ldy + n] = sum_k x[m*ldx + k] * W[n][k] for m < M (M <= 8), W in GGUF Q4_0 (block_bytes 18)
