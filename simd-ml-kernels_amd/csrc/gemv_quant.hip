@@ -45,17 +45,24 @@ constexpr int kThreads = 256;
 // ─── x -> Q8 quants in LDS ───────────────────────────────────────────────────
 
 // Destination dword of quant dword k (values 4k..4k+3) of block b.
+// (The plane offset q * pairs is built from selects: a multiply-add may become v_mad_u64_u32
+// with an undefined high addend half, whose register can be a pending weight load that the
+// compiler then waits for.)
 template <bool kPlanes>
 __device__ __forceinline__ int x_dword_index(int b, int k, int pairs) {
     if (!kPlanes) return 8 * b + k;
-    const int p = b >> 1, q = 2 * (b & 1) + (k >> 2);
-    return 4 * (q * pairs + p) + (k & 3);
+    const int p = b >> 1;
+    const int qp = ((b & 1) ? 2 * pairs : 0) + ((k & 4) ? pairs : 0);  // plane 2 * (b & 1) + (k >> 2)
+    return 4 * (qp + p) + (k & 3);
 }
 
 // One quad of x (4 values of a 32-value block; 8 consecutive threads hold the block) into
 // the LDS quants, bias (Q4_0: -8 * sum of the block's quants) and scale; bad[m] = 1 when the
 // block holds a NaN/Inf.  All 8 threads of the block must call it together (DPP reductions).
-template <bool kPlanes, bool kBias>
+// kChainBias (reference-order Q4_0 kernel): lds_bias gets, per block b and reference lane k
+// (0..3), -8 * the sum of the quants of values {4k..4k+3} and {16+4k..16+4k+3}, at
+// [m * nb * 4 + 4 * b + k].
+template <bool kPlanes, bool kBias, bool kChainBias = false>
 __device__ __forceinline__ void quantize_quad(const float (&v)[4], int m, int kq, int K, uint32_t* lds_q,
                                               int* lds_bias, float* lds_dx, int* bad, bool live = true) {
     const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
@@ -74,8 +81,14 @@ __device__ __forceinline__ void quantize_quad(const float (&v)[4], int m, int kq
     const uint32_t packed = (static_cast<uint32_t>(q[0]) & 0xffu) | ((static_cast<uint32_t>(q[1]) & 0xffu) << 8) |
                             ((static_cast<uint32_t>(q[2]) & 0xffu) << 16) | (static_cast<uint32_t>(q[3]) << 24);
     const int s = kBias ? group_sum_int<8>(q[0] + q[1] + q[2] + q[3]) : 0;
+    int chain = 0;
+    if constexpr (kChainBias) {
+        const int s4 = q[0] + q[1] + q[2] + q[3];
+        chain = -8 * (s4 + __shfl_xor(s4, 4, kWave));  // quads k and k + 4 of the block
+    }
     if (live) {
         lds_q[m * quads + x_dword_index<kPlanes>(b, k, pairs)] = packed;
+        if (kChainBias && k < 4) lds_bias[(m * nb + b) * 4 + k] = chain;
         if (kBias && k == 0) lds_bias[m * nb + b] = -8 * s;
         if (k == 0) lds_dx[m * nb + b] = d;
         if (!fin) bad[m] = 1;
@@ -102,7 +115,7 @@ struct XPreload {
             for (int i = 0; i < 4; ++i) v[p][i] = src[i];
         }
     }
-    template <bool kPlanes, bool kBias>
+    template <bool kPlanes, bool kBias, bool kChainBias = false>
     __device__ __forceinline__ void quantize(const float* __restrict__ x, int ldx, int M, int K, uint32_t* lds_q,
                                              int* lds_bias, float* lds_dx, int* bad) {
         const int quads = K >> 2, total = M * quads;
@@ -114,13 +127,13 @@ struct XPreload {
             const int qd = static_cast<int>(threadIdx.x) + p * NT;
             const bool live = qd < total;
             const int qe = live ? qd : 0, m = qe / quads;
-            quantize_quad<kPlanes, kBias>(v[p], m, qe - m * quads, K, lds_q, lds_bias, lds_dx, bad, live);
+            quantize_quad<kPlanes, kBias, kChainBias>(v[p], m, qe - m * quads, K, lds_q, lds_bias, lds_dx, bad, live);
         }
         for (int qd = static_cast<int>(threadIdx.x) + PQ * NT; qd < total; qd += NT) {
             const int m = qd / quads, kq = qd - m * quads;
             const float* src = x + static_cast<size_t>(m) * ldx + 4 * kq;
             const float t[4] = {src[0], src[1], src[2], src[3]};
-            quantize_quad<kPlanes, kBias>(t, m, kq, K, lds_q, lds_bias, lds_dx, bad);
+            quantize_quad<kPlanes, kBias, kChainBias>(t, m, kq, K, lds_q, lds_bias, lds_dx, bad);
         }
     }
 };
@@ -368,9 +381,7 @@ __host__ __device__ __forceinline__ int ordered_stride(int nb) { return ((nb + 6
 // Integer dot of one reference lane over its eight values: the block's 4 quant bytes (nibble
 // pairs) against x's dword of values {4k..} (xl) and of values {16+4k..} (xh), -8 * sum(x)
 // included.  Exact.
-__device__ __forceinline__ int lane_dot(uint32_t q, uint32_t xl, uint32_t xh) {
-    constexpr uint32_t kMinus8 = 0xF8F8F8F8u;  // four int8 -8
-    const int bias = dot4(kMinus8, xl, dot4(kMinus8, xh, 0));
+__device__ __forceinline__ int lane_dot(uint32_t q, uint32_t xl, uint32_t xh, int bias) {
     return dot4(q & 0x0f0f0f0fu, xl, dot4((q >> 4) & 0x0f0f0f0fu, xh, bias));
 }
 
@@ -394,13 +405,16 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
                                                              int ldx, const uint8_t* __restrict__ W,
                                                              float* __restrict__ y, int ldy, int rows_per_wg,
                                                              int accumulate, const float* __restrict__ norm_w,
-                                                             double norm_eps, int norm_depth, int silu_pairs) {
+                                                             double norm_eps, int norm_depth, int silu_pairs,
+                                                             int nbuf) {
     constexpr int D = 9;
-    constexpr int G = kWave / LPR;           // rows side by side in one wave
+    constexpr int G = kWave / LPR;           // rows side by side in one wave (phase 1)
     constexpr int kWaves = NT / kWave;
     constexpr int kRows = kWaves * G;        // rows of one group
+    constexpr int kChains = 4 * kRows * MT;  // reference lanes of a group (phase 2), at most
+    constexpr int P2 = (kChains + kWave - 1) / kWave;  // waves that run them
     constexpr int PQ = (MT * 1024 + NT - 1) / NT < 4 ? (MT * 1024 + NT - 1) / NT : 4;
-    static_assert(4 * G * MT <= kWave, "phase 2 needs four lanes of the wave per row and row of x");
+    static_assert(P2 <= kWaves, "phase 2 needs four lanes per row and row of x");
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ int bad[MT];
     __shared__ float wave_sum[NT / kWave];
@@ -410,11 +424,14 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
     const size_t row_bytes = static_cast<size_t>(nb) * kQ4_0Bytes;
     uint32_t* lds_q = lds;                                              // M * quads
     float* lds_dx = reinterpret_cast<float*>(lds + M * quads);          // M * nb
-    const int x_words = (M * (quads + nb) + 3) & ~3;
-    int* part = reinterpret_cast<int*>(lds + x_words);                  // [M][kRows][4][S] lane dots
-    float* scl = reinterpret_cast<float*>(part + M * kRows * 4 * S);    // [M][kRows][S] scales
+    int* lds_cb = reinterpret_cast<int*>(lds + ((M * (quads + nb) + 3) & ~3));  // M * nb * 4 lane biases
+    const int x_words = ((M * (quads + nb) + 3) & ~3) + M * nb * 4;
+    // nbuf (1 or 2) buffers of the phase-1 output: [M][kRows][4][S] lane dots (exact integers
+    // as floats), then [M][kRows][S] block scales.
+    float* const part0 = reinterpret_cast<float*>(lds + x_words);
+    const int buf_floats = 5 * M * kRows * S;
 
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int g = lane / LPR, j = lane % LPR;
     const int rl = wave * G + g;             // this lane's row within the group (phase 1)
     const int row0 = blockIdx.x * rows_per_wg;
@@ -439,7 +456,7 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
     if (norm_w) {
         // x and the norm weights first (at most 4 quads a thread: K <= 16 * NT), then the first
         // weights, so that waiting for x does not wait for W.
-        float* xf = scl + M * kRows * S;  // K floats
+        float* xf = part0 + nbuf * buf_floats;  // K floats
         const float4* x4 = reinterpret_cast<const float4*>(x);
         const float4* w4 = reinterpret_cast<const float4*>(norm_w);
         float4 xr[4], wr[4];
@@ -469,7 +486,7 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
             const bool live = qd < quads;
             const float h[4] = {wr[u].x * (xr[u].x * scale), wr[u].y * (xr[u].y * scale),
                                 wr[u].z * (xr[u].z * scale), wr[u].w * (xr[u].w * scale)};
-            quantize_quad<true, false>(h, 0, live ? qd : 0, K, lds_q, nullptr, lds_dx, bad, live);
+            quantize_quad<true, false, true>(h, 0, live ? qd : 0, K, lds_q, lds_cb, lds_dx, bad, live);
         }
         lds_barrier();
     } else {
@@ -479,12 +496,12 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
         __builtin_amdgcn_sched_barrier(0);
         load_group(0, wa);
         __builtin_amdgcn_sched_barrier(0);
-        xp.template quantize<true, false>(x, ldx, M, K, lds_q, nullptr, lds_dx, bad);
+        xp.template quantize<true, false, true>(x, ldx, M, K, lds_q, lds_cb, lds_dx, bad);
         lds_barrier();
     }
 
     // Phase 1 of one pair: the four reference lanes' dots of both blocks, and the scales.
-    auto phase1 = [&](int p, const uint32_t (&w)[D]) {
+    auto phase1 = [&](int p, const uint32_t (&w)[D], float* part, float* scl) {
         uint32_t qa[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) qa[k] = skip2(w[k + 1], w[k]);
@@ -495,80 +512,108 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
                 const uint4* planes = reinterpret_cast<const uint4*>(lds_q + m * quads);
                 const uint4 x0 = planes[p], x1 = planes[pairs + p], x2 = planes[2 * pairs + p],
                             x3 = planes[3 * pairs + p];
-                int* pr = part + (m * kRows + rl) * 4 * S + 2 * p;
-                *reinterpret_cast<int2*>(pr) = make_int2(lane_dot(qa[0], x0.x, x1.x), lane_dot(w[5], x2.x, x3.x));
-                *reinterpret_cast<int2*>(pr + S) = make_int2(lane_dot(qa[1], x0.y, x1.y), lane_dot(w[6], x2.y, x3.y));
-                *reinterpret_cast<int2*>(pr + 2 * S) = make_int2(lane_dot(qa[2], x0.z, x1.z), lane_dot(w[7], x2.z, x3.z));
-                *reinterpret_cast<int2*>(pr + 3 * S) = make_int2(lane_dot(qa[3], x0.w, x1.w), lane_dot(w[8], x2.w, x3.w));
+                const int4 bA = reinterpret_cast<const int4*>(lds_cb + m * nb * 4)[2 * p];
+                const int4 bB = reinterpret_cast<const int4*>(lds_cb + m * nb * 4)[2 * p + 1];
+                float* pr = part + (m * kRows + rl) * 4 * S + 2 * p;
+                auto dots = [&](uint32_t qa_, uint32_t xa, uint32_t xb, int ba, uint32_t qb_, uint32_t xc, uint32_t xd,
+                                int bb) {
+                    return make_float2(static_cast<float>(lane_dot(qa_, xa, xb, ba)),
+                                       static_cast<float>(lane_dot(qb_, xc, xd, bb)));
+                };
+                *reinterpret_cast<float2*>(pr) = dots(qa[0], x0.x, x1.x, bA.x, w[5], x2.x, x3.x, bB.x);
+                *reinterpret_cast<float2*>(pr + S) = dots(qa[1], x0.y, x1.y, bA.y, w[6], x2.y, x3.y, bB.y);
+                *reinterpret_cast<float2*>(pr + 2 * S) = dots(qa[2], x0.z, x1.z, bA.z, w[7], x2.z, x3.z, bB.z);
+                *reinterpret_cast<float2*>(pr + 3 * S) = dots(qa[3], x0.w, x1.w, bA.w, w[8], x2.w, x3.w, bB.w);
                 const float2 d2 = *reinterpret_cast<const float2*>(lds_dx + m * nb + 2 * p);
                 *reinterpret_cast<float2*>(scl + (m * kRows + rl) * S + 2 * p) = make_float2(hA * d2.x, hB * d2.y);
             }
         }
     };
 
-    // Phase 2 of one group, wave by wave: lane (m, g', k) of the wave runs reference lane k's
-    // chain for the wave's row g' against row m of x.
-    auto phase2 = [&](int it) {
-        if (lane < 4 * G * M) {
-            const int m = lane / (4 * G), rg = (lane >> 2) % G, k = lane & 3;
-            const int r = wave * G + rg;
+    // Phase 2 of group it runs on P2 waves, rotating with the group: chain c = 64 * (wave's
+    // turn) + lane is reference lane k = c & 3 of row r = (c >> 2) % kRows against row
+    // m = (c >> 2) / kRows of x; it adds the row's blocks in order, four per LDS read.
+    auto turn_of = [&](int it) {
+        const int t = wave - (it % kWaves) * P2 % kWaves;
+        return t < 0 ? t + kWaves : t;
+    };
+    auto chain_of = [&](int it) { return turn_of(it) * kWave + lane; };
+    // The output such a lane adds to (accumulate), read before the next group's weight loads
+    // are issued, from a clamped index on every lane: its wait never waits for those loads.
+    auto y_prior = [&](int it) {
+        const int c = chain_of(it);
+        const int m = min((c >> 2) / kRows, M - 1);
+        const int row = min(row0 + it * kRows + (c >> 2) % kRows, row_end - 1);
+        return y[static_cast<size_t>(m) * ldy + (silu_pairs ? row >> 1 : row)];
+    };
+
+    auto phase2 = [&](int it, float y_old, const float* part, const float* scl) {
+        const int c = chain_of(it);
+        if (turn_of(it) < P2 && c < 4 * kRows * M) {
+            const int k = c & 3, r = (c >> 2) % kRows, m = (c >> 2) / kRows;
             const int row = row0 + it * kRows + r;
-            const int4* pv = reinterpret_cast<const int4*>(part + ((m * kRows + r) * 4 + k) * S);
+            const float4* pv = reinterpret_cast<const float4*>(part + ((m * kRows + r) * 4 + k) * S);
             const float4* sv = reinterpret_cast<const float4*>(scl + (m * kRows + r) * S);
             float a = 0.0f;
             const int n4 = nb >> 2;
             int q = 0;
             for (; q + 1 < n4; q += 2) {
-                const int4 v0 = pv[q], v1 = pv[q + 1];
+                const float4 v0 = pv[q], v1 = pv[q + 1];
                 const float4 s0 = sv[q], s1 = sv[q + 1];
-                a = fmaf(static_cast<float>(v0.x), s0.x, a);
-                a = fmaf(static_cast<float>(v0.y), s0.y, a);
-                a = fmaf(static_cast<float>(v0.z), s0.z, a);
-                a = fmaf(static_cast<float>(v0.w), s0.w, a);
-                a = fmaf(static_cast<float>(v1.x), s1.x, a);
-                a = fmaf(static_cast<float>(v1.y), s1.y, a);
-                a = fmaf(static_cast<float>(v1.z), s1.z, a);
-                a = fmaf(static_cast<float>(v1.w), s1.w, a);
+                a = fmaf(v0.x, s0.x, a);
+                a = fmaf(v0.y, s0.y, a);
+                a = fmaf(v0.z, s0.z, a);
+                a = fmaf(v0.w, s0.w, a);
+                a = fmaf(v1.x, s1.x, a);
+                a = fmaf(v1.y, s1.y, a);
+                a = fmaf(v1.z, s1.z, a);
+                a = fmaf(v1.w, s1.w, a);
             }
             if (q < n4) {
-                const int4 v0 = pv[q];
+                const float4 v0 = pv[q];
                 const float4 s0 = sv[q];
-                a = fmaf(static_cast<float>(v0.x), s0.x, a);
-                a = fmaf(static_cast<float>(v0.y), s0.y, a);
-                a = fmaf(static_cast<float>(v0.z), s0.z, a);
-                a = fmaf(static_cast<float>(v0.w), s0.w, a);
+                a = fmaf(v0.x, s0.x, a);
+                a = fmaf(v0.y, s0.y, a);
+                a = fmaf(v0.z, s0.z, a);
+                a = fmaf(v0.w, s0.w, a);
             }
             if (nb & 2) {  // nb is even: at most two blocks left
-                const int4 v0 = pv[n4];
+                const float4 v0 = pv[n4];
                 const float4 s0 = sv[n4];
-                a = fmaf(static_cast<float>(v0.x), s0.x, a);
-                a = fmaf(static_cast<float>(v0.y), s0.y, a);
+                a = fmaf(v0.x, s0.x, a);
+                a = fmaf(v0.y, s0.y, a);
             }
             a = a + dpp_f<kDppQuadXor2>(a);   // lanes k and k + 2
             a = a + dpp_f<kDppQuadXor1>(a);   // then the two pair sums
             if (silu_pairs) {
-                // Rows 2n and 2n + 1 are gate_n and up_n (G even, rows of a group aligned):
+                // Rows 2n and 2n + 1 are gate_n and up_n (kRows even, rows of a group aligned):
                 // y[n] = silu(gate_n) * up_n as the reference's SIMD SiLU, then one product.
                 const float up = __shfl_xor(a, 4, kWave);
-                if (k == 0 && (rg & 1) == 0 && row < row_end)
+                if (k == 0 && (r & 1) == 0 && row < row_end)
                     y[static_cast<size_t>(m) * ldy + (row >> 1)] = bad[m] ? __builtin_nanf("") : silu_ref(a) * up;
             } else if (k == 0 && row < row_end) {
                 float* yp = y + static_cast<size_t>(m) * ldy + row;
-                *yp = bad[m] ? __builtin_nanf("") : (accumulate ? *yp + a : a);
+                *yp = bad[m] ? __builtin_nanf("") : (accumulate ? y_old + a : a);
             }
         }
     };
 
+    // One group: every wave's phase 1 into the group's buffer, a workgroup barrier, phase 2
+    // on P2 waves.  With two buffers the next group's phase 1 overlaps this phase 2 (the
+    // barrier after it orders the reuse of this buffer); with one, a second barrier does.
     auto body = [&](int it, uint32_t (&cur)[CH][D], uint32_t (&nxt)[CH][D]) {
+        const float y_old = y_prior(it);
         load_group(it + 1 < iters ? it + 1 : it, nxt);  // the last group reloads its own (cached) bytes
+        float* part = part0 + (nbuf == 2 ? (it & 1) * buf_floats : 0);
+        float* scl = part + 4 * M * kRows * S;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int p = j + c * LPR;
-            if (p < pairs) phase1(p, cur[c]);
+            if (p < pairs) phase1(p, cur[c], part, scl);
         }
-        wave_lds_sync();  // this wave's rows are complete in LDS
-        phase2(it);
-        wave_lds_sync();  // read before the next group overwrites them
+        lds_barrier();
+        phase2(it, y_old, part, scl);
+        if (nbuf == 1) lds_barrier();
     };
 
     int it = 0;
@@ -823,10 +868,10 @@ hipError_t launch_generic(int M, int N, int K, const float* x, int ldx, const ui
 
 inline bool accumulate_unsupported(int acc) { return acc != 0; }  // the SiLU-pair epilogue overwrites
 
-size_t ordered_lds_bytes(int M, int K, int rows_per_group) {
+size_t ordered_lds_bytes(int M, int K, int rows_per_group, int nbuf = 1) {
     const size_t nb = static_cast<size_t>(K) >> 5, quads = static_cast<size_t>(K) >> 2;
-    const size_t x_words = (M * (quads + nb) + 3) & ~static_cast<size_t>(3);
-    return 4 * x_words + static_cast<size_t>(M) * rows_per_group * ordered_stride(static_cast<int>(nb)) * 20;
+    const size_t x_words = ((M * (quads + nb) + 3) & ~static_cast<size_t>(3)) + M * nb * 4;
+    return 4 * x_words + static_cast<size_t>(nbuf) * M * rows_per_group * ordered_stride(static_cast<int>(nb)) * 20;
 }
 
 struct NormArgs {
@@ -842,12 +887,16 @@ hipError_t launch_ordered_ch(int M, int N, int K, const float* x, int ldx, const
     constexpr int kRows = NT / LPR;
     if (nrm.w && (M != 1 || (8 << nrm.depth) > NT)) return hipErrorInvalidValue;
     if (nrm.silu_pairs && (LPR > 32 || (rows_per_wg & 1) || accumulate_unsupported(acc))) return hipErrorInvalidValue;
-    const size_t lds = ordered_lds_bytes(M, K, kRows) + (nrm.w ? static_cast<size_t>(K) * 4 : 0);
     if (rows_per_wg <= 0) rows_per_wg = std::max(kRows, (N + 511) / 512);
+    const size_t extra = nrm.w ? static_cast<size_t>(K) * 4 : 0;
+    // Two phase-1 buffers (phase 2 of a group overlaps the next group's phase 1) when a
+    // workgroup has several groups and they fit.
+    const int nbuf = (rows_per_wg > kRows && ordered_lds_bytes(M, K, kRows, 2) + extra <= 150 * 1024) ? 2 : 1;
+    const size_t lds = ordered_lds_bytes(M, K, kRows, nbuf) + extra;
     const int grid = (N + rows_per_wg - 1) / rows_per_wg;
     if (const hipError_t e = allow_lds(gemv_q4_ordered_kernel<LPR, MT, NT, CH>, lds); e != hipSuccess) return e;
     hipLaunchKernelGGL((gemv_q4_ordered_kernel<LPR, MT, NT, CH>), dim3(grid), dim3(NT), lds, stream, M, N, K, x, ldx,
-                       W, y, ldy, rows_per_wg, acc, nrm.w, nrm.eps, nrm.depth, nrm.silu_pairs);
+                       W, y, ldy, rows_per_wg, acc, nrm.w, nrm.eps, nrm.depth, nrm.silu_pairs, nbuf);
     return hipGetLastError();
 }
 
@@ -930,21 +979,25 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
     }
     // The lane split does not change the result here (every row's sum has the reference's
     // order), so it is chosen for speed only.
-    int lpr = (t && t->lanes_per_row) ? t->lanes_per_row : (pairs >= 128 ? 64 : pairs >= 16 ? 16 : 8);
+    // Measured on MI355X: one workgroup per compute unit (its groups pipelined through two
+    // phase-1 buffers), 32 lanes per row up to 32 pairs a row and 64 beyond, and the fewest
+    // threads (256 to 1024) whose group covers the workgroup's rows.
+    int lpr = (t && t->lanes_per_row) ? t->lanes_per_row : (pairs >= 64 ? 64 : pairs >= 16 ? 32 : 16);
     while (lpr < 64 && (pairs + lpr - 1) / lpr > 8) lpr *= 2;  // at most 8 pairs per lane and row
     int rpw = t ? t->rows_per_wg : 0;
+    if (rpw <= 0) {
+        rpw = std::max(1, (N + g_cus - 1) / g_cus);
+        rpw += rpw & 1;  // (gate, up) pairs of the SiLU epilogue never straddle workgroups
+    }
     if (mt == 1) {
-        const double bytes = static_cast<double>(N) * (K >> 5) * kQ4_0Bytes;
-        const int per_cu = bytes < 24e6 ? 1 : (bytes < 128e6 ? 2 : 4);
-        if (rpw <= 0) rpw = std::max(1, (N + g_cus * per_cu - 1) / (g_cus * per_cu));
         if (nrm.silu_pairs) {
-            rpw += rpw & 1;            // (gate, up) pairs never straddle workgroups
-            if (lpr > 32) lpr = 32;    // and two rows at least side by side in a wave
+            if (rpw & 1) return hipErrorInvalidValue;
+            if (lpr > 32) lpr = 32;    // two rows at least side by side in a wave
         }
-        int nt = (t && t->threads) ? t->threads : ((bytes < 24e6 || bytes >= 128e6) ? 1024 : 512);
+        int nt = (t && t->threads) ? t->threads : 256;
         const size_t cap = kLdsCap - (nrm.w ? static_cast<size_t>(K) * 4 : 0);
         if (!(t && t->threads)) {
-            while (nt > 256 && nt > rpw * lpr) nt /= 2;
+            while (nt < 1024 && nt < rpw * lpr) nt *= 2;
             while (nt > 256 && ordered_lds_bytes(1, K, nt / lpr) > cap) nt /= 2;
         }
         while (ordered_lds_bytes(1, K, nt / lpr) > cap && lpr < (nrm.silu_pairs ? 32 : 64)) lpr *= 2;
@@ -956,8 +1009,8 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
             default: return launch_ordered_lpr<1, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream, nrm);
         }
     }
-    // Several rows of x: 256 threads, 32 or 64 lanes per row (phase 2 needs 4 * rows * M lanes).
-    const bool l32 = ordered_lds_bytes(M, K, 256 / 32) <= kLdsCap && lpr <= 32;
+    // Several rows of x: 256 threads, 32 or 64 lanes per row (phase 2 needs 4 * rows * M <= 256).
+    const bool l32 = ordered_lds_bytes(M, K, 256 / 32) <= kLdsCap && (!(t && t->lanes_per_row) || lpr <= 32);
     switch (mt) {
         case 2: return l32 ? launch_ordered<32, 2, 256>(M, N, K, x, ldx, W, y, ldy, rpw, acc, stream)
                            : launch_ordered<64, 2, 256>(M, N, K, x, ldx, W, y, ldy, rpw, acc, stream);
