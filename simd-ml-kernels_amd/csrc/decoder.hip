@@ -88,9 +88,11 @@ __global__ void embed_kernel(const uint8_t* __restrict__ E, int type, int hidden
 //   out = sk.sgemm(p, V): the AVX2 direct product (avx2_gemm_packed.cpp:151-201), one fused
 //     chain over the positions in order per output.
 // One workgroup of 256 threads per query head; scores in LDS; cached K and V read in tiles of
-// kTile positions staged through LDS (the K and V tiles of a round are loaded together).
+// `tile` positions staged through LDS (up to kMaxTile; every position of a decode that fits
+// one tile is read in the first round, together with q, k and v).
 constexpr int kAttnThreads = 256;
-constexpr int kTile = 128;
+constexpr int kMaxTile = 256;
+constexpr size_t kAttnLdsBudget = 150 * 1024;
 
 // count floats (a multiple of 4, 16-byte aligned ends) from global to LDS: every thread issues
 // its 16-byte loads of a round before storing any (no load waits for an earlier store).
@@ -141,7 +143,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
                                                                  const float* __restrict__ sin_tab, int interleaved,
                                                                  float* __restrict__ kc, float* __restrict__ vc,
                                                                  int n_heads, int n_kv, int hd, int cap, float scale,
-                                                                 const DecodeState* __restrict__ st,
+                                                                 int tile, const DecodeState* __restrict__ st,
                                                                  float* __restrict__ out) {
     extern __shared__ float sc[];  // T scores then probabilities; then the K and V tiles
     __shared__ float qs[256], ks[256], vs[256];
@@ -155,13 +157,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     const int pos = st->pos, T = pos + 1;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     constexpr int kWaves = kAttnThreads / kWave;
-    float* ktile = sc + ((cap + 3) & ~3);   // kTile * hd
-    float* vtile = ktile + kTile * hd;      // kTile * hd
+    float* ktile = sc + ((cap + 3) & ~3);   // tile * hd
+    float* vtile = ktile + tile * hd;       // tile * hd
     float* K = kc + static_cast<size_t>(g) * cap * hd;
     float* V = vc + static_cast<size_t>(g) * cap * hd;
     // This step's q, k, v and the first round's cached K and V (positions < pos), all loads
     // issued before any store.
-    const int first_cached = min(min(kTile, T), pos);
+    const int first_cached = min(min(tile, T), pos);
     {
         const int d = threadIdx.x;
         float q0 = 0.0f, k0 = 0.0f, v0 = 0.0f;
@@ -171,7 +173,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
             v0 = qkv[static_cast<size_t>(n_heads + n_kv + g) * hd + d];
         }
         const int n4 = first_cached * hd / 4;
-        constexpr int kPer = 8;  // float4 per thread of one tile (kTile * 64 / 4 / 256); more rounds if larger
+        constexpr int kPer = 16;  // float4 per thread: 256 positions of head_dim 64 (larger: the loop below)
         float4 ka[kPer], va[kPer];
         const float4* k4 = reinterpret_cast<const float4*>(K);
         const float4* v4 = reinterpret_cast<const float4*>(V);
@@ -210,17 +212,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
             K[static_cast<size_t>(pos) * hd + d] = ks[d];
             V[static_cast<size_t>(pos) * hd + d] = vs[d];
         }
-    // Scores and the V tiles, kTile positions a round.  Position pos comes from ks / vs.
+    // Scores and the V tiles, `tile` positions a round.  Position pos comes from ks / vs.
     const int l = threadIdx.x & 15;
-    for (int t0 = 0; t0 < T; t0 += kTile) {
-        const int tn = min(kTile, T - t0);
+    for (int t0 = 0; t0 < T; t0 += tile) {
+        const int tn = min(tile, T - t0);
         const int cached = min(tn, pos - t0);  // positions of this round read from the cache
         __syncthreads();  // the previous round's tiles are consumed
         if (cached > 0 && t0 > 0) stage_tiles(ktile, K + static_cast<size_t>(t0) * hd, nullptr, nullptr, cached * hd);
         if (cached < tn)
             for (int d = threadIdx.x; d < hd; d += kAttnThreads) ktile[(pos - t0) * hd + d] = ks[d];
         __syncthreads();
-        for (int tt = threadIdx.x >> 4; tt < kTile; tt += kAttnThreads / 16) {
+        for (int tb = 0; tb < tn; tb += kAttnThreads / 16) {  // uniform bound: every lane reaches the DPP
+            const int tt = tb + (threadIdx.x >> 4);
             const int tc = min(tt, tn - 1);
             const float* kr = ktile + tc * hd;
             float a0 = 0.0f, a1 = 0.0f;
@@ -228,11 +231,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
                 if (p + l < hd) a0 = fmaf(qs[p + l], kr[p + l], a0);
                 if (p + 16 + l < hd) a1 = fmaf(qs[p + 16 + l], kr[p + 16 + l], a1);
             }
+            // Lane 0 of the 16 gets ((s0 + s8) + (s4 + s12)) + ... as the reference's halving
+            // reduce (lanes i and i+8, then i+4, i+2, i+1), the partners read through DPP.
             float v = a0 + a1;
-            v = v + __shfl_xor(v, 8, 16);
-            v = v + __shfl_xor(v, 4, 16);
-            v = v + __shfl_xor(v, 2, 16);
-            v = v + __shfl_xor(v, 1, 16);
+            v = v + dpp_f<kDppRowShl8>(v);
+            v = v + dpp_f<kDppRowShl4>(v);
+            v = v + dpp_f<kDppRowShl2>(v);
+            v = v + dpp_f<kDppRowShl1>(v);
             if (l == 0 && tt < tn) sc[t0 + tt] = scale * v;
         }
     }
@@ -290,8 +295,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     // out[d] = one fused chain over the positions in order.
     float acc = 0.0f;
     const int d = threadIdx.x;
-    for (int t0 = 0; t0 < T; t0 += kTile) {
-        const int tn = min(kTile, T - t0);
+    for (int t0 = 0; t0 < T; t0 += tile) {
+        const int tn = min(tile, T - t0);
         const int cached = min(tn, pos - t0);
         __syncthreads();  // probabilities written / the previous tile consumed
         if (cached > 0 && t0 > 0) stage_tiles(vtile, V + static_cast<size_t>(t0) * hd, nullptr, nullptr, cached * hd);
@@ -306,7 +311,16 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     if (d < hd) out[static_cast<size_t>(head) * hd + d] = acc;
 }
 
-size_t attention_lds(int cap, int hd) { return (static_cast<size_t>((cap + 3) & ~3) + 2 * static_cast<size_t>(kTile) * hd) * 4; }
+// Positions per round: the whole cache when it fits kMaxTile, else as many as the LDS budget
+// leaves beside the scores (at least 16).
+int attention_tile(int cap, int hd) {
+    const size_t left = kAttnLdsBudget / 4 - static_cast<size_t>((cap + 3) & ~3);
+    const int fit = static_cast<int>(left / (2 * static_cast<size_t>(hd)));
+    return std::max(16, std::min({kMaxTile, cap, fit}));
+}
+size_t attention_lds(int cap, int hd) {
+    return (static_cast<size_t>((cap + 3) & ~3) + 2 * static_cast<size_t>(attention_tile(cap, hd)) * hd) * 4;
+}
 
 // m = silu(g) * u (llama.py:434: sk.silu(gate) * up, two float32 results multiplied), SiLU as
 // the reference's SIMD tables compute it.
@@ -543,7 +557,7 @@ hipError_t enqueue_step(Model& md, bool with_logits, Marks* mk = nullptr) {
         SMK_MARK(kAttention);
         hipLaunchKernelGGL(attention_kernel, dim3(nh), dim3(kAttnThreads), attention_lds(md.capacity, hd), s,
                            md.qkv, md.cos_tab, md.sin_tab, c.rope_interleaved, kc, vc, nh, nkv, hd, md.capacity,
-                           scale, md.st, md.attn);
+                           scale, attention_tile(md.capacity, hd), md.st, md.attn);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         SMK_MARK(kGemvO);
         if ((e = gemv(L.o, md.attn, md.x, true, s)) != hipSuccess) return e;

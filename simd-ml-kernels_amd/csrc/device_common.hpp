@@ -49,6 +49,12 @@ constexpr int kDppQuadXor1 = 0xB1;
 constexpr int kDppQuadXor2 = 0x4E;
 constexpr int kDppHalfMirror = 0x141;
 constexpr int kDppRowMirror = 0x140;
+// row_shl:n -- lane i of a 16-lane row reads lane i + n of the row (lanes past the row's end
+// read 0): a halving reduction whose result is wanted in the row's first lane only.
+constexpr int kDppRowShl1 = 0x101;
+constexpr int kDppRowShl2 = 0x102;
+constexpr int kDppRowShl4 = 0x104;
+constexpr int kDppRowShl8 = 0x108;
 
 template <int ctrl>
 __device__ __forceinline__ int dpp_i(int v) {
