@@ -25,42 +25,46 @@ __device__ __forceinline__ float elem_to_float(const void* base, size_t i) {
     else return bf16_bits_to_float(static_cast<const uint16_t*>(base)[i]);
 }
 
-// 8 consecutive elements of B widened to FP32.
+// 16 bytes of a row of B as loaded (8 fp16 / bf16 values, or 4 fp32), widened at use.
 template <int E>
-__device__ __forceinline__ void load8(const void* row, size_t k, float (&v)[8]) {
-    if constexpr (E == 0) {
-        const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(row) + k);
-        const f32x4 a = p[0], b = p[1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else {
-        const u32x4 t = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(row) + k);
-        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+__device__ __forceinline__ void widen(const u32x4& t, float* v) {
+    const uint32_t w[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if constexpr (E == 1) {
-                v[2 * i] = half_bits_to_float(w[i]);
-                v[2 * i + 1] = half_bits_to_float(w[i] >> 16);
-            } else {
-                v[2 * i] = __uint_as_float(w[i] << 16);
-                v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-            }
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (E == 0) {
+            v[i] = __uint_as_float(w[i]);
+        } else if constexpr (E == 1) {
+            v[2 * i] = half_bits_to_float(w[i]);
+            v[2 * i + 1] = half_bits_to_float(w[i] >> 16);
+        } else {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
         }
     }
 }
 
-template <int E, int LPR, int U, int MT>
+// LPR lanes share a row; a lane takes 8-element groups j, j + LPR, ... of its U rows.  The
+// loads of the next D groups are issued before the current D groups' FMAs (two register
+// buffers), every load unconditional from a clamped row and group so the compiler's wait
+// counts stay exact.  FP32 B takes two 16-byte loads per group.
+template <int E, int LPR, int U, int MT, int D>
 __global__ __launch_bounds__(kThreads) void gemv_lowp_kernel(int M, int N, int K, float alpha,
                                                              const void* __restrict__ A, int lda,
                                                              const void* __restrict__ B, int ldb, float beta,
-                                                             float* __restrict__ C, int ldc, int kt) {
+                                                             float* __restrict__ C, int ldc, int kt, int a_vec) {
     constexpr int G = kWave / LPR;
     constexpr int kRowsPerWg = 4 * G * U;
+    constexpr int L = E == 0 ? 2 : 1;             // 16-byte loads per 8-element group
+    constexpr size_t kEs = E == 0 ? 4 : 2;
     extern __shared__ __align__(16) float4 xs[];  // [MT][2][kt/8]
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int g = lane / LPR, j = lane % LPR;
     const int rb = blockIdx.x * kRowsPerWg + wave * G * U + g;
     const int groups_max = kt / 8;
+    const char* rows[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        rows[u] = static_cast<const char*>(B) + static_cast<size_t>(min(rb + u * G, N - 1)) * ldb * kEs;
 
     float acc[U][MT];
 #pragma unroll
@@ -71,34 +75,81 @@ __global__ __launch_bounds__(kThreads) void gemv_lowp_kernel(int M, int N, int K
     for (int k0 = 0; k0 < K; k0 += kt) {
         const int klen = min(kt, K - k0);
         const int groups = klen / 8;
-        __syncthreads();
-        for (int i = threadIdx.x; i < M * klen; i += blockDim.x) {
-            const int m = i / klen, k = i - m * klen;
-            const float v = elem_to_float<E>(A, static_cast<size_t>(m) * lda + k0 + k);
-            const int grp = k >> 3, h = (k >> 2) & 1, e = k & 3;
-            reinterpret_cast<float*>(xs + (m * 2 + h) * groups_max + grp)[e] = v;
-        }
-        __syncthreads();
-        for (int c = j; c < groups; c += LPR) {
-            float w[U][8];
+        const int steps = (groups + LPR - 1) / LPR;  // groups of this lane: c = j + i * LPR, i < steps
+        auto load = [&](int i0, u32x4 (&w)[D][U][L]) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int r = rb + u * G;
-                if (r < N) {
-                    const char* row = static_cast<const char*>(B) + static_cast<size_t>(r) * ldb * (E == 0 ? 4 : 2);
-                    load8<E>(row, static_cast<size_t>(k0) + 8 * c, w[u]);
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                if (m >= M) continue;
-                const float4 xa = xs[(m * 2) * groups_max + c], xb = xs[(m * 2 + 1) * groups_max + c];
-                const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            for (int d = 0; d < D; ++d) {
+                const int c = min(j + (i0 + d) * LPR, groups - 1);
 #pragma unroll
                 for (int u = 0; u < U; ++u)
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[u][m] = fmaf(xv[e], w[u][e], acc[u][m]);
+                    for (int h = 0; h < L; ++h)
+                        w[d][u][h] = reinterpret_cast<const u32x4*>(rows[u] + (static_cast<size_t>(k0) + 8 * c) * kEs)[h];
             }
+        };
+        u32x4 wa[D][U][L], wb[D][U][L];
+        load(0, wa);  // both buffers are issued before the A tile is staged (whose loads wait
+        load(D, wb);  // for everything issued earlier)
+        __syncthreads();
+        // A tile: 8-element groups, four loaded per thread before any is stored (16-byte loads
+        // when A's rows are 16-byte aligned), so its loads wait together once.
+        const int ng = M * groups;
+        for (int i0 = threadIdx.x; i0 < ng; i0 += 4 * kThreads) {
+            float v[4][8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int i = min(i0 + q * kThreads, ng - 1);
+                const int m = i / groups, grp = i - m * groups;
+                const size_t base = static_cast<size_t>(m) * lda + k0 + 8 * grp;
+                if (a_vec) {
+                    const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const char*>(A) + base * kEs);
+                    widen<E>(p[0], v[q]);
+                    if constexpr (L == 2) widen<E>(p[1], v[q] + 4);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[q][e] = elem_to_float<E>(A, base + e);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int i = i0 + q * kThreads;
+                if (i < ng) {
+                    const int m = i / groups, grp = i - m * groups;
+                    xs[(m * 2) * groups_max + grp] = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+                    xs[(m * 2 + 1) * groups_max + grp] = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
+                }
+            }
+        }
+        __syncthreads();
+        auto compute = [&](int i0, const u32x4 (&w)[D][U][L]) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                const int c = j + (i0 + d) * LPR;
+                if (c < groups) {
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        if (m >= M) continue;
+                        const float4 xa = xs[(m * 2) * groups_max + c], xb = xs[(m * 2 + 1) * groups_max + c];
+                        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+                        for (int u = 0; u < U; ++u) {
+                            float wv[8];
+                            widen<E>(w[d][u][0], wv);
+                            if constexpr (L == 2) widen<E>(w[d][u][1], wv + 4);
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) acc[u][m] = fmaf(xv[e], wv[e], acc[u][m]);
+                        }
+                    }
+                }
+            }
+        };
+        // Every pass issues the same loads (past the end they reload the last group, cached), so
+        // the wait before a buffer's FMAs counts exactly the other buffer's loads.
+        for (int i0 = 0; i0 < steps; i0 += 2 * D) {
+            compute(i0, wa);
+            load(i0 + 2 * D, wa);
+            compute(i0 + D, wb);
+            load(i0 + 3 * D, wb);
         }
     }
 #pragma unroll
@@ -171,14 +222,17 @@ template <int E, int LPR, int U, int MT>
 hipError_t launch_lowp(int M, int N, int K, float alpha, const void* A, int lda, const void* B, int ldb, float beta,
                        float* C, int ldc, hipStream_t s) {
     constexpr int kRowsPerWg = 4 * (kWave / LPR) * U;
+    constexpr int D = E == 0 ? 2 : 4;  // groups per lane and row in flight per buffer (two buffers)
     // A tile in LDS: at most 64 KiB (MT rows of kt floats), kt a multiple of 8.
     int kt = std::min(K, (65536 / (4 * std::max(M, 1))) / 8 * 8);
     kt = std::max(kt, 8);
     const size_t lds = static_cast<size_t>(MT) * kt * 4;
     const int grid = (N + kRowsPerWg - 1) / kRowsPerWg;
-    if (const hipError_t e = allow_lds(gemv_lowp_kernel<E, LPR, U, MT>, lds); e != hipSuccess) return e;
-    hipLaunchKernelGGL((gemv_lowp_kernel<E, LPR, U, MT>), dim3(grid), dim3(kThreads), lds, s, M, N, K, alpha, A, lda,
-                       B, ldb, beta, C, ldc, kt);
+    if (const hipError_t e = allow_lds(gemv_lowp_kernel<E, LPR, U, MT, D>, lds); e != hipSuccess) return e;
+    constexpr size_t es = E == 0 ? 4 : 2;
+    const int a_vec = reinterpret_cast<uintptr_t>(A) % 16 == 0 && (static_cast<size_t>(lda) * es) % 16 == 0;
+    hipLaunchKernelGGL((gemv_lowp_kernel<E, LPR, U, MT, D>), dim3(grid), dim3(kThreads), lds, s, M, N, K, alpha, A,
+                       lda, B, ldb, beta, C, ldc, kt, a_vec);
     return hipGetLastError();
 }
 

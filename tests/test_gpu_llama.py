@@ -68,6 +68,25 @@ def test_tiny_engine_matches_reference_loop(tmp_path, wname):
         m.close()
 
 
+def test_tiny_long_context_several_attention_rounds(tmp_path):
+    """A cache of 600 positions is read in rounds of 256 (the K / V tiles); logits stay
+    bit-identical with the reference loop past the first round."""
+    path, prompt, dec = _tiny(tmp_path, "q4_0", seed=26)
+    rng = np.random.default_rng(26)
+    seq = prompt + [int(t) for t in rng.integers(0, TINY["vocab_size"], 292)]
+    m = llama.Llama(str(tmp_path), gguf=path)
+    try:
+        m.reset(600)
+        dec.reset(600)
+        for i, t in enumerate(seq):
+            lg = m.step(t)
+            lo = dec.step(t)
+            if i >= 240 or i % 37 == 0:
+                np.testing.assert_array_equal(lg.view(np.uint32), lo.view(np.uint32), err_msg=f"position {i}")
+    finally:
+        m.close()
+
+
 def test_tiny_module_loop_matches_engine(tmp_path):
     path, prompt, _ = _tiny(tmp_path, "q4_0", seed=22)
     eng = llama.Llama(str(tmp_path), gguf=path)
