@@ -191,7 +191,8 @@ int smk_runtime_version(int* runtime, int* built);
 
 /* Diagnostics: force the quantized GEMV's lanes per row, rows per workgroup, threads per
  * workgroup and per-step row unroll (0 = automatic; the last two apply to one row of x),
- * and report the kernel a call would use ("pairs" or "generic"). */
+ * and report the kernel a call would use ("pairs" or "generic").  Lanes per row 16, 32 or 64
+ * and unroll 2 or 4 also set the FP16 / BF16 / FP32 GEMV's (smk_d_gemm_tb, up to 8 rows). */
 int smk_set_gemv_tuning(int lanes_per_row, int rows_per_wg, int threads, int unroll);
 /* Diagnostics: 1 (default) sums every Q4_0 row in the reference's SIMD order (q4_0_rows.hpp:
  * y bit-exact with its AVX2 / AVX-512 tables); 0 selects the free-order kernel, whose y is

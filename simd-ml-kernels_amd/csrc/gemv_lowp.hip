@@ -17,6 +17,7 @@ namespace smk {
 namespace {
 
 constexpr int kThreads = 256;
+int g_lowp_lpr = 0, g_lowp_unroll = 0;
 
 template <int E>
 __device__ __forceinline__ float elem_to_float(const void* base, size_t i) {
@@ -239,10 +240,23 @@ hipError_t launch_lowp(int M, int N, int K, float alpha, const void* A, int lda,
 template <int E, int MT>
 hipError_t lowp_mt(int M, int N, int K, float alpha, const void* A, int lda, const void* B, int ldb, float beta,
                    float* C, int ldc, hipStream_t s) {
-    // Lanes per row from the row length in 8-element groups.
+    if (g_lowp_lpr) {  // diagnostics: forced lanes per row and rows per lane group
+        const bool u4 = g_lowp_unroll >= 4;
+        switch (g_lowp_lpr) {
+            case 64: return u4 ? launch_lowp<E, 64, 4, MT>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s)
+                               : launch_lowp<E, 64, 2, MT>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
+            case 32: return u4 ? launch_lowp<E, 32, 4, MT>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s)
+                               : launch_lowp<E, 32, 2, MT>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
+            case 16: return u4 ? launch_lowp<E, 16, 4, MT>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s)
+                               : launch_lowp<E, 16, 2, MT>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
+            default: break;
+        }
+    }
+    // Lanes per row from the row length in 8-element groups, two rows per lane group
+    // (measured on MI355X at the Llama-3-8B shapes).
     const int groups = K / 8;
-    if (groups >= 64) return launch_lowp<E, 64, 4, MT>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
-    if (groups >= 32) return launch_lowp<E, 32, 4, MT>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
+    if (groups > 512) return launch_lowp<E, 64, 2, MT>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
+    if (groups >= 32) return launch_lowp<E, 32, 2, MT>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
     if (groups >= 16) return launch_lowp<E, 16, 2, MT>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
     return launch_lowp<E, 8, 2, MT>(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, s);
 }
@@ -266,6 +280,11 @@ hipError_t gemm_tb_e(int M, int N, int K, float alpha, const void* A, int lda, c
 }
 
 }  // namespace
+
+void set_lowp_tuning(int lanes_per_row, int unroll) {
+    g_lowp_lpr = lanes_per_row;
+    g_lowp_unroll = unroll;
+}
 
 hipError_t gemm_tb(int elem, int M, int N, int K, float alpha, const void* A, int lda, const void* B, int ldb,
                    float beta, float* C, int ldc, hipStream_t s) {

@@ -36,6 +36,10 @@ hipError_t gemv_quant(int block_bytes, int M, int N, int K, const float* x, int 
 // Compute units of the device (workgroup counts of the GEMV follow it).
 void set_compute_units(int cus);
 
+// Diagnostics: lanes per row (16, 32 or 64; 0 automatic) and rows per lane group (2 or 4) of
+// the FP16 / BF16 / FP32 GEMV.
+void set_lowp_tuning(int lanes_per_row, int unroll);
+
 // The kernel gemv_quant would launch, for reports: "pairs" or "generic".
 const char* gemv_quant_path(int block_bytes, int N, int K, const uint8_t* W);
 

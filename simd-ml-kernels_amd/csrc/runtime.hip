@@ -717,6 +717,7 @@ int smk_set_gemv_tuning(int lanes_per_row, int rows_per_wg, int threads, int unr
     g_tuning.rows_per_wg = rows_per_wg;
     g_tuning.threads = threads;
     g_tuning.unroll = unroll;
+    smk::set_lowp_tuning(lanes_per_row >= 16 ? lanes_per_row : 0, unroll);
     return ok();
 }
 
