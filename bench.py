@@ -4,7 +4,8 @@
 Headline (BASELINE.json metric "Q4_0 GEMV weight GB/s & % of HBM peak"): the Q4_0
 decode GEMV y = x @ W.T at the Llama-3.2-1B FFN up/gate shape N=8192, K=2048
 x ~ N(0,1), W ~ N(0,0.02) quantized to GGUF Q4_0 by this
-library's bit-exact quantizer, seed 0.  A step is one GEMV launch on the next of
+library's bit-exact quantizer, seed 0, summed in the reference's SIMD order (y bit-exact
+with its AVX2 / AVX-512 tables).  A step is one GEMV launch on the next of
 ceil(512 MiB / 9.4 MB) + 1 distinct device copies of W, so the 256 MB Infinity
 Cache never holds the weights; inputs are resident in HBM before timing starts.
 Steps are launched back to back on one stream and timed with HIP events recorded
@@ -12,9 +13,12 @@ on that same stream; the launch loop is captured in a HIP graph (mode "graph",
 default) or issued from Python (mode "stream").
 
 The JSON line also carries the other GEMV configurations (Q8_0 both orientations,
-FP16/BF16 and Q4_0 at Llama-3-8B shapes, the Q4_0 lm_head), the measured HBM read
-roof, the roofline of the headline kernel and the CPU baseline: the REFERENCE's own
-best SIMD path (oracle/_ref, built from its sources) on this host's cores.
+FP16/BF16 and Q4_0 at Llama-3-8B shapes, the Q4_0 lm_heads, the Llama-3.2-1B decode
+shapes, batched rows M = 2, 4, 8, the headline shape in free summation order), the
+measured HBM read roof, the roofline of the headline kernel, the decode of BASELINE
+config 5 (128 greedy tokens of the synthetic Llama-3.2-1B through the device engine,
+token-checked against the reference's CPU loop) and the CPU baseline: the REFERENCE's
+own best SIMD path (oracle/_ref, built from its sources) on this host's cores.
 """
 
 from __future__ import annotations
@@ -319,6 +323,17 @@ def main() -> int:
             for N, K in ((14336, 4096), (4096, 14336), (4096, 4096)):
                 cases[f"{fmt}_{N}x{K}"] = lowp_case(dev, fmt, N, K, 2, max(60, st // 8), 10, args.mode)
         cases["q4_0_lm_head_128256x4096"] = quant_case(dev, "q4_0", 128256, 4096, 3, 40, 4, args.mode)
+        # The Llama-3.2-1B decode GEMVs (fused q|k|v, o, fused gate|up, down, lm_head) as plain calls.
+        for N, K in ((3072, 2048), (2048, 2048), (16384, 2048), (2048, 8192)):
+            cases[f"q4_0_{N}x{K}"] = quant_case(dev, "q4_0", N, K, 5, st, wu, args.mode)
+        cases["q4_0_lm_head_128256x2048"] = quant_case(dev, "q4_0", 128256, 2048, 5, 60, 6, args.mode)
+        # The headline shape with the free-order kernel (y within the reference's error bound, not
+        # its bits): the cost of summing in the reference's SIMD order.
+        dev.abi.call("smk_set_q4_order", 0)
+        try:
+            cases["q4_0_8192x2048_free_order"] = quant_case(dev, "q4_0", 8192, 2048, 0, st, wu, args.mode)
+        finally:
+            dev.abi.call("smk_set_q4_order", 1)
         for M in (2, 4, 8):
             cases[f"q4_0_M{M}_14336x4096"] = quant_case(dev, "q4_0", 14336, 4096, 4, st, wu, args.mode, M=M)
     roof = read_roof(dev)
