@@ -47,7 +47,9 @@ def parse():
     p.add_argument("--steps", type=int, default=2000, help="timed GEMV launches of the headline case")
     p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--mode", choices=["graph", "stream"], default="graph")
-    p.add_argument("--cases", choices=["all", "headline"], default="all")
+    p.add_argument("--cases", choices=["all", "headline", "decode-eager"], default="all",
+                   help="decode-eager: only the decode model, its 159 positions stepped one kernel "
+                        "at a time with per-section events (a profiler-friendly breakdown)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     return p.parse_args()
@@ -303,6 +305,38 @@ def cpu_baseline(N: int, K: int, budget_s: float) -> dict | None:
                       f"{len(copies)} rotated host copies ({len(copies) * wq.nbytes / 2 ** 20:.0f} MiB); {path}; {model}"}
 
 
+def decode_eager() -> dict:
+    """The decode model of decode_case, teacher-forced through its 159 positions (prompt + golden
+    tokens) with eager, individually launched kernels and an event at each section start
+    (smk_llama_step_profile): the per-section device time per token."""
+    import shutil
+    import tempfile
+
+    from simd_ml_kernels import llama
+
+    with open(GOLDEN_TOKENS) as f:
+        gold = json.load(f)
+    tmp = tempfile.mkdtemp(prefix="smk_llama_", dir="/tmp")
+    try:
+        path, prompt = llama.write_synthetic_model(tmp, gold["config"], seed=gold["seed"],
+                                                   n_prompt=len(gold["prompt"]))
+        m = llama.Llama(tmp, gguf=path)
+        try:
+            seq = prompt + gold["tokens"][:-1]
+            m.profile = {}
+            m.reset(len(seq))
+            for t in seq:
+                m.step(t)
+            p = m.profile
+        finally:
+            m.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    n = p["steps"]
+    return {"positions": n, "ms_per_token": round(1e3 * p["total"] / n, 4),
+            "us_per_token": {k: round(1e6 * v / n, 1) for k, v in p["device"].items()}}
+
+
 def main() -> int:
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -310,6 +344,9 @@ def main() -> int:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}, "
               f"WORLD_SIZE {world}).", file=sys.stderr)
         return 2
+    if args.cases == "decode-eager":
+        print(json.dumps({"decode_eager": decode_eager()}))
+        return 0
     dev = Dev()
     head = quant_case(dev, "q4_0", 8192, 2048, 0, args.steps, args.warmup, args.mode)
     cases = {}
