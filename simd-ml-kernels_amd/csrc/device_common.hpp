@@ -55,6 +55,7 @@ constexpr int kDppRowShl1 = 0x101;
 constexpr int kDppRowShl2 = 0x102;
 constexpr int kDppRowShl4 = 0x104;
 constexpr int kDppRowShl8 = 0x108;
+constexpr int kDppRowRor8 = 0x128;  // row_ror:8 -- lane i of a row reads lane i ^ 8
 
 template <int ctrl>
 __device__ __forceinline__ int dpp_i(int v) {

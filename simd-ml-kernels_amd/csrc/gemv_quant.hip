@@ -124,6 +124,7 @@ struct XPreload {
         // into, past the weight loads.
 #pragma unroll
         for (int p = 0; p < PQ; ++p) {
+            if (p * NT >= total) break;  // uniform: no thread has a quad this far
             const int qd = static_cast<int>(threadIdx.x) + p * NT;
             const bool live = qd < total;
             const int qe = live ? qd : 0, m = qe / quads;
@@ -482,6 +483,7 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
         const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(var) + norm_eps));
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
+            if (u * NT >= quads) break;  // uniform: no thread has a quad this far
             const int qd = static_cast<int>(threadIdx.x) + u * NT;
             const bool live = qd < quads;
             const float h[4] = {wr[u].x * (xr[u].x * scale), wr[u].y * (xr[u].y * scale),

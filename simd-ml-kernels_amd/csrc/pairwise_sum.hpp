@@ -38,12 +38,17 @@ __device__ __forceinline__ float uniform_chunk_sum(const float* __restrict__ q, 
     if (l < leaves) {
         leaf_of(l, depth, n, start, len);
         const int full = len - (len % 8);
-        float v = q[start + k];
-        r = v * v;
-        for (int i = 8 + k; i < full; i += 8) {
-            v = q[start + i];
-            r = r + v * v;
+        // Leaves hold at most 128 values (16 per lane): every read is issued before the sums.
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int i = 8 * j + k;
+            v[j] = i < full ? q[start + i] : 0.0f;
         }
+        r = v[0] * v[0];
+#pragma unroll
+        for (int j = 1; j < 16; ++j)
+            if (8 * j + k < full) r = r + v[j] * v[j];
     }
     r = r + dpp_f<kDppQuadXor1>(r);
     r = r + dpp_f<kDppQuadXor2>(r);
@@ -54,8 +59,11 @@ __device__ __forceinline__ float uniform_chunk_sum(const float* __restrict__ q, 
             r = r + v * v;
         }
     }
-    // Sibling leaves: lanes xor 8, 16, 32 hold leaves l^1, l^2, l^4 of the same wave.
-    for (int lv = 0; lv < 3 && (2 << lv) <= leaves; ++lv) r = r + __shfl_xor(r, 8 << lv, kWave);
+    // Sibling leaves: lanes xor 8, 16, 32 hold leaves l^1, l^2, l^4 of the same wave (xor 8 is a
+    // rotation by 8 inside a 16-lane DPP row, xor 16 a swizzle inside 32 lanes).
+    if (leaves >= 2) r = r + dpp_f<kDppRowRor8>(r);
+    if (leaves >= 4) r = r + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(r), 0x401f));
+    if (leaves >= 8) r = r + __shfl_xor(r, 32, kWave);
     if ((threadIdx.x & (kWave - 1)) == 0) wave_sum[threadIdx.x / kWave] = r;
     __syncthreads();
     const int used = leaves >= 8 ? leaves / 8 : 1;  // waves that hold leaves
