@@ -87,6 +87,31 @@ def test_tiny_long_context_several_attention_rounds(tmp_path):
         m.close()
 
 
+MID = dict(TINY, hidden_size=2048, intermediate_size=8192, num_attention_heads=32, num_key_value_heads=8,
+           head_dim=64)
+
+
+def test_mid_model_logits_equal_reference_loop(tmp_path):
+    """Llama-3.2-1B layer widths (K = 2048 and 8192, the shapes of the fused GEMV launches) with
+    two layers: logits bit-identical with the reference loop at every position, through the fused
+    RMSNorm prologues and the SiLU and residual epilogues."""
+    path, prompt = llama.write_synthetic_model(str(tmp_path), MID, seed=27, n_prompt=6, weight_type=gguf.Q4_0)
+    c = lr.Cfg.from_config(MID)
+    oprompt, W = lr.synthetic_model(c, 27, 6, lr.Q4_0)
+    assert prompt == oprompt
+    dec = lr.Decoder(c, W, lr.Q4_0, _oracle_kind())
+    seq = prompt + [11, 222, 333]
+    m = llama.Llama(str(tmp_path), gguf=path)
+    try:
+        m.reset(len(seq))
+        dec.reset(len(seq))
+        for i, t in enumerate(seq):
+            np.testing.assert_array_equal(m.step(t).view(np.uint32), dec.step(t).view(np.uint32),
+                                          err_msg=f"position {i}")
+    finally:
+        m.close()
+
+
 def test_tiny_module_loop_matches_engine(tmp_path):
     path, prompt, _ = _tiny(tmp_path, "q4_0", seed=22)
     eng = llama.Llama(str(tmp_path), gguf=path)
