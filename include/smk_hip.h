@@ -91,7 +91,10 @@ int smk_weights_stats(size_t* bytes, int* entries);
 /* ─── Device-pointer entry points (async on `stream`) ─────────────────────── */
 int smk_d_gemv_q4_0(int N, int K, const float* x, const uint8_t* Wq, float* y, void* stream);
 int smk_d_gemv_q8_0(int N, int K, const float* x, const uint8_t* Wq, float* y, void* stream);
-/* Rows m < M (M <= 8) of X [M, ldx] against the same W: Y [M, ldy]. */
+/* Rows m < M of X [M, ldx] against the same W: Y [M, ldy]; row m of Y equals the one-row call
+ * on row m of X bit for bit.  Q4_0 with M >= 2 (K % 64 == 0) runs on the matrix cores, with a
+ * scratch buffer the library keeps per stream (allocated on a stream's first call of a larger
+ * size; that call must not be made while the stream is captured into a graph). */
 int smk_d_gemm_q4_0(int M, int N, int K, const float* X, int ldx, const uint8_t* Wq, float* Y, int ldy, void* stream);
 int smk_d_gemm_q8_0(int M, int N, int K, const float* X, int ldx, const uint8_t* Wq, float* Y, int ldy, void* stream);
 /* elem: 0 FP32, 1 FP16, 2 BF16.  C = beta C + alpha A B^T, A [M, lda], B [N, ldb]. */
@@ -198,6 +201,10 @@ int smk_set_gemv_tuning(int lanes_per_row, int rows_per_wg, int threads, int unr
  * y bit-exact with its AVX2 / AVX-512 tables); 0 selects the free-order kernel, whose y is
  * within the reference's error bound, for speed comparisons. */
 int smk_set_q4_order(int reference_order);
+/* Diagnostics: rows of X from which a Q4_0 product (smk_gemm_q4_0, smk_d_gemm_q4_0) takes the
+ * matrix-core kernel (0 = built-in choice; a large value keeps the launches of 8 GEMV rows).
+ * No reference counterpart: the reference has no batched Q4_0 product (pybind_entry.cpp:956-957). */
+int smk_set_q4_mfma_min_rows(int rows);
 const char* smk_gemv_path(int K, const void* Wq);
 
 #ifdef __cplusplus

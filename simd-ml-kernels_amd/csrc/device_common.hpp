@@ -127,6 +127,25 @@ __device__ __forceinline__ int round_half_away(float v) {
     return static_cast<int>(t) + (r >= 0.5f ? 1 : 0) - (r <= -0.5f ? 1 : 0);
 }
 
+// Q8 quants of one quad of x (values 4k..4k+3 of a 32-value block whose 8 quads sit in 8
+// consecutive lanes, which call this together): quantize_row_q8_0 (q8_0_scalar.cpp:237-256)
+// -- d = amax / 127 (IEEE division), id = 1 / d (0 when d is 0 or 1/d overflows float,
+// q8_0_scalar.cpp:249-252), q = round half away from zero (v * id), every product rounded on
+// its own.  fin = 0 when one of the quad's values is a NaN or an infinity; such a quad keeps
+// q = 0.  Returns the four quants as bytes of one dword, value 4k in the low byte.
+__device__ __forceinline__ uint32_t q8_quad(const float (&v)[4], float& d, int (&q)[4], int& fin) {
+    fin = finite_bits(v[0]) & finite_bits(v[1]) & finite_bits(v[2]) & finite_bits(v[3]);
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = group_max<8>(amax);
+    d = amax / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    if (!(id <= 3.40282347e38f)) id = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = fin ? round_half_away(v[i] * id) : 0;
+    return (static_cast<uint32_t>(q[0]) & 0xffu) | ((static_cast<uint32_t>(q[1]) & 0xffu) << 8) |
+           ((static_cast<uint32_t>(q[2]) & 0xffu) << 16) | (static_cast<uint32_t>(q[3]) << 24);
+}
+
 // The reference's vectorised exp (simd_math.hpp:63-117, used by its SiLU and softmax): clamp
 // to +-88.3762626647949 (a NaN becomes the bound, as vminps/vmaxps return their second
 // operand), k = floor(z*log2e + 0.5) with one fused multiply-add, Cody-Waite reduction

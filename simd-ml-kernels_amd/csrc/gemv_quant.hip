@@ -41,6 +41,12 @@ namespace {
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr int kThreads = 256;
+// Rows of x from which a Q4_0 product takes the matrix-core kernel.  Measured on MI355X
+// (graph-replayed, us, matrix-core / 8-row GEMV launches): 14336x4096 M=2 19.7/20.0, M=4
+// 19.7/31.4, M=8 26.5/57.3, M=32 65/229; 8192x2048 M=2 11.9/9.3, M=4 12.1/13.6; 2048x8192
+// (128 row tiles for 256 CUs) M=4 30.6/28.6, M=8 43.6/192.
+constexpr int kMfmaMinRows = 4;
+inline bool mfma_rows_pay(int M, int N) { return M > 4 || (M == 4 && N >= 4096); }
 
 // ─── x -> Q8 quants in LDS ───────────────────────────────────────────────────
 
@@ -67,19 +73,9 @@ __device__ __forceinline__ void quantize_quad(const float (&v)[4], int m, int kq
                                               int* lds_bias, float* lds_dx, int* bad, bool live = true) {
     const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
     const int b = kq >> 3, k = kq & 7;
-    const int fin = finite_bits(v[0]) & finite_bits(v[1]) & finite_bits(v[2]) & finite_bits(v[3]);
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = group_max<8>(amax);
-    const float d = amax / 127.0f;                 // IEEE division (correctly rounded)
-    float id = d != 0.0f ? 1.0f / d : 0.0f;
-    if (!(id <= 3.40282347e38f)) id = 0.0f;        // 1/d overflows: q = 0 (q8_0_scalar.cpp:249-252)
-    int q[4] = {0, 0, 0, 0};
-    if (fin) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) q[i] = round_half_away(v[i] * id);
-    }
-    const uint32_t packed = (static_cast<uint32_t>(q[0]) & 0xffu) | ((static_cast<uint32_t>(q[1]) & 0xffu) << 8) |
-                            ((static_cast<uint32_t>(q[2]) & 0xffu) << 16) | (static_cast<uint32_t>(q[3]) << 24);
+    float d;
+    int q[4], fin;
+    const uint32_t packed = q8_quad(v, d, q, fin);
     const int s = kBias ? group_sum_int<8>(q[0] + q[1] + q[2] + q[3]) : 0;
     int chain = 0;
     if constexpr (kChainBias) {
@@ -1081,7 +1077,7 @@ hipError_t fill(float* y, long long n, float value, hipStream_t stream) {
 hipError_t gemv_quant(int block_bytes, int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y,
                       int ldy, hipStream_t stream, const GemvTuning* tuning) {
     if (N <= 0 || M <= 0) return hipSuccess;
-    if (M > 8 || K < 0 || K % 32 != 0) return hipErrorInvalidValue;
+    if (K < 0 || K % 32 != 0) return hipErrorInvalidValue;
     if (K == 0) {
         if (tuning && tuning->accumulate) return hipSuccess;  // y + 0
         for (int m = 0; m < M; ++m) {
@@ -1091,6 +1087,21 @@ hipError_t gemv_quant(int block_bytes, int M, int N, int K, const float* x, int 
         return hipSuccess;
     }
     if (block_bytes != kQ4_0Bytes && block_bytes != kQ8_0Bytes) return hipErrorInvalidValue;
+    if (block_bytes == kQ4_0Bytes && M > 1 && !(tuning && (tuning->unordered || tuning->norm_w || tuning->silu_pairs)) &&
+        (tuning && tuning->mfma_min_rows ? M >= tuning->mfma_min_rows : (M >= kMfmaMinRows && mfma_rows_pay(M, N)))) {
+        // Several rows of x on the matrix cores; the last row of an odd N (its own order) goes
+        // through the one-row kernels below.
+        const int ne = N & ~1;
+        if (ne > 0 && gemm_q4_mfma_ok(M, ne, K, W)) {
+            void* ws = nullptr;
+            if (const hipError_t e = stream_workspace(stream, gemm_q4_mfma_workspace(M, K), &ws); e != hipSuccess)
+                return e;
+            const hipError_t e = gemm_q4_mfma(M, ne, K, x, ldx, W, y, ldy, tuning ? tuning->accumulate : 0, ws, stream);
+            if (e != hipSuccess || ne == N) return e;
+            const size_t row_bytes = static_cast<size_t>(K >> 5) * kQ4_0Bytes;
+            return gemv_quant(block_bytes, M, 1, K, x, ldx, W + ne * row_bytes, y + ne, ldy, stream, tuning);
+        }
+    }
     // The x quants of one launch live in LDS (K + 8*K/32 bytes per row of x): split the rows of
     // x so that each launch fits in 144 KiB of the CU's 160 KiB.
     const size_t per_row = static_cast<size_t>(K) + 8 * static_cast<size_t>(K >> 5);

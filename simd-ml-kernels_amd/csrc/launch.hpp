@@ -25,13 +25,31 @@ struct GemvTuning {
     double norm_eps = 0.0;          // (numpy-exact, as rms_norm), K <= 8192, N even
     int silu_pairs = 0;             // Q4_0, one row of x, N even: rows 2n, 2n+1 are (gate, up);
                                     // y[n] = silu(gate) * up (y has N / 2 entries)
+    int mfma_min_rows = 0;          // Q4_0 in the reference order: rows of x from which the
+                                    // matrix-core kernel takes the product (0: built-in choice)
 };
 
-// y[m*ldy + n] = sum_k x[m*ldx + k] * W[n][k] for m < M (M <= 8), W in GGUF Q4_0 (block_bytes 18)
-// or Q8_0 (34) blocks; each row of x is quantized to Q8 blocks inside the kernel.  A row of x
-// with a NaN or +-Inf makes its whole row of y NaN; K == 0 gives zeros.  K % 32 == 0.
+// y[m*ldy + n] = sum_k x[m*ldx + k] * W[n][k] for m < M, W in GGUF Q4_0 (block_bytes 18) or
+// Q8_0 (34) blocks; each row of x is quantized to Q8 blocks (inside the GEMV kernel, or once
+// by the batched Q4_0 path's quantizer).  A row of x with a NaN or +-Inf makes its whole row
+// of y NaN; K == 0 gives zeros.  K % 32 == 0.  Several rows of x against Q4_0 take the matrix-core
+// kernel (gemm_q4_mfma) when its shape conditions hold, with the stream's scratch buffer
+// (stream_workspace); otherwise launches of at most 8 rows.
 hipError_t gemv_quant(int block_bytes, int M, int N, int K, const float* x, int ldx, const uint8_t* W,
                       float* y, int ldy, hipStream_t stream, const GemvTuning* tuning = nullptr);
+
+// The batched Q4_0 product on the matrix cores, every row bit-identical with the one-row
+// reference-order kernel: M >= 1 rows of x, N even, K % 64 == 0, W 4-byte aligned
+// (gemm_q4_mfma_ok).  workspace: gemm_q4_mfma_workspace(M, K) bytes of device memory, 16-byte
+// aligned, used by the launches on `stream` only.  acc: y = y + x.W^T.
+bool gemm_q4_mfma_ok(int M, int N, int K, const uint8_t* W);
+size_t gemm_q4_mfma_workspace(int M, int K);
+hipError_t gemm_q4_mfma(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy, int acc,
+                        void* workspace, hipStream_t stream);
+// A scratch buffer of at least `bytes` owned by the library for launches on `stream` of the
+// current device (grown outside graph capture only: the first call of a size must not be
+// captured).
+hipError_t stream_workspace(hipStream_t stream, size_t bytes, void** out);
 
 // Compute units of the device (workgroup counts of the GEMV follow it).
 void set_compute_units(int cus);

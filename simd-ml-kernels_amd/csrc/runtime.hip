@@ -249,8 +249,9 @@ int host_gemm_quant(int bb, int M, int N, int K, const float* X, const uint8_t* 
     if (const int rc = context(&c)) return rc;
     const void* wd;
     if (const int rc = weights_on_device(c, Wq, static_cast<size_t>(N) * (K / 32) * bb, &wd)) return rc;
-    for (int m0 = 0; m0 < M; m0 += 8) {
-        const int mr = std::min(8, M - m0);
+    // Rows of X in uploads of at most 32 (one matrix-core launch at K <= 4096).
+    for (int m0 = 0; m0 < M; m0 += 32) {
+        const int mr = std::min(32, M - m0);
         if (const int rc = upload(c, c->a, X + static_cast<size_t>(m0) * K, static_cast<size_t>(mr) * K * 4)) return rc;
         SMK_HIP(c->c.reserve(static_cast<size_t>(mr) * N * 4), "device scratch");
         SMK_HIP(smk::gemv_quant(bb, mr, N, K, static_cast<const float*>(c->a.p), K, static_cast<const uint8_t*>(wd),
@@ -485,7 +486,6 @@ static hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
 static int d_gemm_quant(int bb, int M, int N, int K, const float* X, int ldx, const uint8_t* Wq, float* Y, int ldy,
                         void* stream) {
     if (const int rc = check_gemv_args(M, N, K, X, Wq, Y)) return rc;
-    if (M > 8) return fail(SMK_ERR_ARGUMENT, "M must be <= 8 on the device entry point");
     if (M > 0 && (ldx < K || ldy < N)) return fail(SMK_ERR_ARGUMENT, "ldx >= K and ldy >= N required");
     if (reinterpret_cast<uintptr_t>(X) % 4 || reinterpret_cast<uintptr_t>(Wq) % 2 || reinterpret_cast<uintptr_t>(Y) % 4)
         return fail(SMK_ERR_ARGUMENT, "X and Y must be 4-byte aligned and Wq 2-byte aligned");
@@ -703,6 +703,12 @@ int smk_runtime_version(int* runtime, int* built) {
 int smk_set_q4_order(int reference_order) {
     if (reference_order != 0 && reference_order != 1) return fail(SMK_ERR_ARGUMENT, "reference_order must be 0 or 1");
     g_tuning.unordered = reference_order ? 0 : 1;
+    return ok();
+}
+
+int smk_set_q4_mfma_min_rows(int rows) {
+    if (rows < 0) return fail(SMK_ERR_ARGUMENT, "rows must be >= 0");
+    g_tuning.mfma_min_rows = rows;
     return ok();
 }
 

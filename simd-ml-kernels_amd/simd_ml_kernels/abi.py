@@ -100,6 +100,7 @@ SIGNATURES = {
     "smk_runtime_version": [ctypes.POINTER(_i), ctypes.POINTER(_i)],
     "smk_set_gemv_tuning": [_i, _i, _i, _i],
     "smk_set_q4_order": [_i],
+    "smk_set_q4_mfma_min_rows": [_i],
     "smk_gemv_path": [_i, _p],
 }
 _RESTYPE = {"smk_last_error": ctypes.c_char_p, "smk_version": ctypes.c_char_p, "smk_gemv_path": ctypes.c_char_p}

@@ -243,6 +243,118 @@ class TestBatched:
             np.testing.assert_array_equal(Y[m].view(np.uint32), y1.view(np.uint32))
 
 
+def d_gemm(fmt, X, wq, N, K, offset=0):
+    """Y [M, N] from smk_d_gemm_<fmt> on device copies (Wq `offset` bytes into its buffer); the
+    4 KiB after Y must stay untouched."""
+    M = X.shape[0]
+    staged = np.full(wq.nbytes + offset + 16, 0xEE, np.uint8)
+    staged[offset:offset + wq.nbytes] = wq.reshape(-1)
+    xd, wd, yd = g.dev(X), g.dev(staged), g.dev(np.full(M * N + 1024, 0xEEEEEEEE, np.uint32))
+    g.call(f"smk_d_gemm_{fmt}", M, N, K, g.ptr(xd), K, g.ptr(wd, offset), g.ptr(yd), N, g.stream())
+    out = g.host(yd, np.uint32, M * N + 1024)
+    assert (out[M * N:] == 0xEEEEEEEE).all(), "wrote past Y"
+    return out[:M * N].view(np.float32).reshape(M, N)
+
+
+class TestBatchedMatrixCores:
+    """Q4_0 with several rows of x runs on the int8 matrix cores (gemm_q4_mfma.hip); every row must
+    equal the reference's SIMD order for that row (oracle/smk_oracle.c, pinned to the reference's
+    AVX-512 build) bit for bit -- the exact integer block sums, the four FMA chains per output and
+    the final (a0 + a2) + (a1 + a3)."""
+
+    # (M, N, K, W byte offset): K % 1024 == 0 with a 16-byte aligned W takes the streaming kernel,
+    # the rest (K % 64 == 0, W 4-byte aligned) the whole-image kernel; odd N ends in the one-row
+    # kernels; one launch holds 4, 8, 16 or 32 rows of x.
+    CASES = [(2, 96, 4096, 0), (3, 64, 2048, 0), (4, 130, 64, 0), (5, 48, 128, 0), (8, 96, 4096, 0),
+             (9, 32, 2048, 0), (16, 64, 4096, 0), (17, 80, 1024, 0), (31, 16, 2048, 0), (32, 200, 4096, 0),
+             (33, 50, 4096, 0), (64, 34, 2048, 0), (12, 40, 14336, 0), (20, 18, 8192, 0), (7, 97, 2048, 0),
+             (32, 1, 4096, 0), (6, 64, 2048, 4), (32, 48, 1088, 0), (13, 36, 4096, 4)]
+
+    @pytest.fixture(autouse=True)
+    def _matrix_cores_from_two_rows(self):
+        g.call("smk_set_q4_mfma_min_rows", 2)
+        yield
+        g.call("smk_set_q4_mfma_min_rows", 0)
+
+    @pytest.mark.parametrize("M,N,K,off", CASES)
+    def test_rows_bit_exact_with_reference_order(self, M, N, K, off):
+        rng = np.random.default_rng(M * 1000 + N + K)
+        X = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+        wq = o.quantize_q4_0((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+        Y = d_gemm("q4_0", X, wq, N, K, offset=off)
+        for m in range(M):
+            ref = o.gemv_q4_0_simd(X[m], wq, N, K)
+            np.testing.assert_array_equal(Y[m].view(np.uint32), ref.view(np.uint32), err_msg=f"row {m}")
+
+    @pytest.mark.parametrize("M", [2, 4, 8, 32])
+    def test_equals_eight_row_gemv_path(self, M):
+        """The matrix-core path, the 8-row GEMV launches and the built-in switch give the same bits."""
+        N, K = 256, 4096
+        rng = np.random.default_rng(M)
+        X = rng.standard_normal((M, K)).astype(np.float32)
+        wq = o.quantize_q4_0(rng.standard_normal((N, K)).astype(np.float32))
+        Y = d_gemm("q4_0", X, wq, N, K)
+        g.call("smk_set_q4_mfma_min_rows", 1 << 30)
+        Y8 = d_gemm("q4_0", X, wq, N, K)
+        g.call("smk_set_q4_mfma_min_rows", 0)
+        Yd = d_gemm("q4_0", X, wq, N, K)
+        np.testing.assert_array_equal(Y.view(np.uint32), Y8.view(np.uint32))
+        np.testing.assert_array_equal(Y.view(np.uint32), Yd.view(np.uint32))
+
+    def test_nonfinite_rows_and_extremes(self):
+        """A row of x with a NaN or an infinity is NaN, the others exact; saturated quants
+        (x blocks at +-amax, weight nibbles 0 and 15) stay exact."""
+        M, N, K = 12, 64, 2048
+        rng = np.random.default_rng(4)
+        X = rng.standard_normal((M, K)).astype(np.float32)
+        X[3, 100] = np.nan
+        X[7, 2047] = -np.inf
+        X[9] = np.where(rng.standard_normal(K) > 0, 1.0, -1.0).astype(np.float32) * 1e30
+        X[10] = 0.0
+        w = rng.standard_normal((N, K)).astype(np.float32)
+        w[::2] = np.where(w[::2] > 0, 1.0, -1.0) * np.abs(w[::2]).max()
+        wq = o.quantize_q4_0(w)
+        Y = d_gemm("q4_0", X, wq, N, K)
+        for m in range(M):
+            ref = o.gemv_q4_0_simd(X[m], wq, N, K)
+            if m in (3, 7):
+                assert np.isnan(Y[m]).all() and np.isnan(ref).all()
+            else:
+                np.testing.assert_array_equal(Y[m].view(np.uint32), ref.view(np.uint32), err_msg=f"row {m}")
+
+    def test_two_byte_aligned_w_takes_gemv_path(self):
+        M, N, K = 6, 40, 2048
+        rng = np.random.default_rng(6)
+        X = rng.standard_normal((M, K)).astype(np.float32)
+        wq = o.quantize_q4_0(rng.standard_normal((N, K)).astype(np.float32))
+        Y = d_gemm("q4_0", X, wq, N, K, offset=2)
+        for m in range(M):
+            np.testing.assert_array_equal(Y[m].view(np.uint32), o.gemv_q4_0_simd(X[m], wq, N, K).view(np.uint32))
+
+    def test_config_4_shape(self):
+        """BASELINE config 4 at M = 32: N = 14336, K = 4096, x ~ N(0,1), W ~ N(0,0.02); every row
+        against the one-row device GEMV (itself bit-exact with the reference order), eight rows
+        against the oracle."""
+        M, N, K = 32, 14336, 4096
+        X, w = o.synthetic(4, [(M, K), (N, K)], [1.0, 0.02])
+        wq = o.quantize_q4_0(w)
+        del w
+        Y = d_gemm("q4_0", X, wq, N, K)
+        for m in range(M):
+            np.testing.assert_array_equal(Y[m].view(np.uint32), d_gemv("q4_0", X[m], wq, N, K).view(np.uint32))
+        for m in (0, 5, 17, 31):
+            np.testing.assert_array_equal(Y[m].view(np.uint32), o.gemv_q4_0_simd(X[m], wq, N, K).view(np.uint32))
+
+    def test_q8_0_more_than_eight_rows(self):
+        M, N, K = 13, 70, 2048
+        rng = np.random.default_rng(13)
+        X = rng.standard_normal((M, K)).astype(np.float32)
+        wq = o.quantize_q8_0(rng.standard_normal((N, K)).astype(np.float32))
+        Y = d_gemm("q8_0", X, wq, N, K)
+        for m in range(M):
+            np.testing.assert_array_equal(Y[m].view(np.uint32), d_gemv("q8_0", X[m], wq, N, K).view(np.uint32))
+
+
 class TestBaselineShapes:
     """Full BASELINE.json configurations, checked against the exact float64 sum."""
 
