@@ -47,9 +47,11 @@ def parse():
     p.add_argument("--steps", type=int, default=2000, help="timed GEMV launches of the headline case")
     p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--mode", choices=["graph", "stream"], default="graph")
-    p.add_argument("--cases", choices=["all", "headline", "decode-eager"], default="all",
-                   help="decode-eager: only the decode model, its 159 positions stepped one kernel "
-                        "at a time with per-section events (a profiler-friendly breakdown)")
+    p.add_argument("--cases", choices=["all", "headline", "decode", "batched", "decode-eager"], default="all",
+                   help="decode: only the decode model; batched: only the config 4 Q4_0 products "
+                        "(M = 1, 2, 4, 8, 32 at 14336x4096, both kernels); decode-eager: only the decode "
+                        "model, its 159 positions stepped one kernel at a time with per-section events "
+                        "(a profiler-friendly breakdown)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     return p.parse_args()
@@ -142,6 +144,22 @@ def quant_case(dev: Dev, fmt: str, N: int, K: int, seed: int, steps: int, warmup
             "GBps_weights_x_y": (nbytes + 4 * M * (K + N)) / sec / 1e9, "GFLOPs": 2 * M * N * K / sec / 1e9}
 
 
+def batched_cases(dev: Dev, steps: int, warmup: int, mode: str) -> dict:
+    """Q4_0 at N=14336, K=4096 for M = 2, 4, 8, 32 rows of x (M = 1 is the
+    q4_0_14336x4096 case), each through the built-in choice (the int8 matrix-core kernel from
+    M = 3 at this N) and through launches of 8 GEMV rows, the switch point's other side."""
+    out = {}
+    for M in (2, 4, 8, 32):
+        out[f"q4_0_M{M}_14336x4096"] = quant_case(dev, "q4_0", 14336, 4096, 4, steps, warmup, mode, M=M)
+        dev.abi.call("smk_set_q4_mfma_min_rows", 1 << 30)
+        try:
+            out[f"q4_0_M{M}_14336x4096_gemv_rows"] = quant_case(dev, "q4_0", 14336, 4096, 4, max(40, steps // 4),
+                                                                10, mode, M=M)
+        finally:
+            dev.abi.call("smk_set_q4_mfma_min_rows", 0)
+    return out
+
+
 def lowp_case(dev: Dev, fmt: str, N: int, K: int, seed: int, steps: int, warmup: int, mode: str):
     rng = np.random.default_rng(seed)
     x = rng.standard_normal(K, dtype=np.float32)
@@ -229,6 +247,14 @@ def decode_case(runs: int = 3) -> dict:
                 ids = list(m.generate(prompt, gold["n_new"], stats=st, stop_at_eos=False))
                 tps.append(st["decode_steps"] / st["decode_s"])
                 pre.append(st["prefill_s"] / st["prefill_tokens"])
+            # The prompt one graph step per token (the reference loop's prefill), for comparison.
+            m.set_prefill_rows(0)
+            pre_tok = []
+            ids_tok = None
+            for _ in range(runs):
+                st = {}
+                ids_tok = list(m.generate(prompt, gold["n_new"], stats=st, stop_at_eos=False))
+                pre_tok.append(st["prefill_s"] / st["prefill_tokens"])
             wb = m.weight_bytes()
         finally:
             m.close()
@@ -239,6 +265,9 @@ def decode_case(runs: int = 3) -> dict:
             "prompt_tokens": len(prompt), "new_tokens": gold["n_new"], "decode_tok_s": round(tok_s, 1),
             "runs_tok_s": [round(v, 1) for v in tps], "ms_per_token": round(1e3 / tok_s, 4),
             "prefill_ms_per_token": round(1e3 * float(np.median(pre)), 4),
+            "prefill": "one 32-row chunk: matrix-core Q4_0 products over the rows",
+            "prefill_token_by_token_ms_per_token": round(1e3 * float(np.median(pre_tok)), 4),
+            "tokens_equal_token_by_token_prefill": ids_tok == ids,
             "gemv_weight_bytes_per_token": int(wb),
             "gemv_weight_GBps": round(wb * tok_s / 1e9, 1), "pct_hbm_peak": round(100 * wb * tok_s / PEAK_HBM, 2),
             "tokens_match_reference_cpu_loop": ids == gold["tokens"], "model_write_s": round(t_write, 1)}
@@ -347,7 +376,13 @@ def main() -> int:
     if args.cases == "decode-eager":
         print(json.dumps({"decode_eager": decode_eager()}))
         return 0
+    if args.cases == "decode":
+        print(json.dumps({"decode": decode_case()}))
+        return 0
     dev = Dev()
+    if args.cases == "batched":
+        print(json.dumps({"batched": batched_cases(dev, max(200, args.steps // 4), 50, args.mode)}))
+        return 0
     head = quant_case(dev, "q4_0", 8192, 2048, 0, args.steps, args.warmup, args.mode)
     cases = {}
     if args.cases == "all":
@@ -371,8 +406,7 @@ def main() -> int:
             cases["q4_0_8192x2048_free_order"] = quant_case(dev, "q4_0", 8192, 2048, 0, st, wu, args.mode)
         finally:
             dev.abi.call("smk_set_q4_order", 1)
-        for M in (2, 4, 8):
-            cases[f"q4_0_M{M}_14336x4096"] = quant_case(dev, "q4_0", 14336, 4096, 4, st, wu, args.mode, M=M)
+        cases.update(batched_cases(dev, st, wu, args.mode))
     roof = read_roof(dev)
     copy = copy_roof(dev)
     decode = decode_case() if args.cases == "all" else None

@@ -162,6 +162,11 @@ int smk_llama_step(void* model, int token, float* logits);
  * out: the n_new generated ids; seconds (optional, 2 doubles): prefill and decode time. */
 int smk_llama_generate(void* model, const int* prompt, int n_prompt, int n_new, int* out, double* seconds);
 int smk_llama_info(void* model, int* position, int* capacity, unsigned long long* weight_bytes);
+/* Prompt of smk_llama_generate in chunks of `rows` rows (default 64; 0 or 1: one graph step per
+ * prompt token, as the reference's loop, llama.py:491-492).  A chunk runs every matrix product
+ * on all its rows at once (Q4_0: the matrix-core kernel); the KV cache and the generated tokens
+ * are the same bit for bit either way.  Quantized matrices only (FP32 models run token by token). */
+int smk_llama_set_prefill_rows(void* model, int rows);
 /* step() run eagerly with a HIP event at every section start (the engine's counterpart of
  * llama.py:441-479, _step_profiled); adds each section's milliseconds into section_ms[0..11):
  * embed, rms_norm, gemv_qkv, rope_kv, attention, gemv_o, gemv_gate_up, silu_mul, gemv_down,

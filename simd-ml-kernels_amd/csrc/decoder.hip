@@ -45,10 +45,8 @@ struct DecodeState {
 
 // x = row `token` of the embedding (llama.py:337 / gguf_reader.py:112-129: d * (q - 8) for
 // Q4_0, d * q for Q8_0, the float32 row for F32; every product is exact in float32).
-__global__ void embed_kernel(const uint8_t* __restrict__ E, int type, int hidden, int vocab,
-                             const int* __restrict__ tokens, const DecodeState* __restrict__ st,
-                             float* __restrict__ x) {
-    int tok = tokens[st->pos];
+__device__ __forceinline__ void embed_row(const uint8_t* __restrict__ E, int type, int hidden, int vocab, int tok,
+                                          float* __restrict__ x) {
     tok = min(max(tok, 0), vocab - 1);  // host checks every token; a bad one must not fault
     const int nb = hidden >> 5;
     for (int i = threadIdx.x; i < hidden; i += blockDim.x) {
@@ -71,6 +69,18 @@ __global__ void embed_kernel(const uint8_t* __restrict__ E, int type, int hidden
         }
         x[i] = v;
     }
+}
+
+__global__ void embed_kernel(const uint8_t* __restrict__ E, int type, int hidden, int vocab,
+                             const int* __restrict__ tokens, const DecodeState* __restrict__ st,
+                             float* __restrict__ x) {
+    embed_row(E, type, hidden, vocab, tokens[st->pos], x);
+}
+
+// Rows p < gridDim.x of a prompt chunk: x[p] = row tokens[p] of the embedding.
+__global__ void embed_rows_kernel(const uint8_t* __restrict__ E, int type, int hidden, int vocab,
+                                  const int* __restrict__ tokens, float* __restrict__ x) {
+    embed_row(E, type, hidden, vocab, tokens[blockIdx.x], x + static_cast<size_t>(blockIdx.x) * hidden);
 }
 
 // Grouped-query attention of one query head over positions 0..pos (llama.py:398-412) with the
@@ -144,7 +154,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
                                                                  float* __restrict__ kc, float* __restrict__ vc,
                                                                  int n_heads, int n_kv, int hd, int cap, float scale,
                                                                  int tile, const DecodeState* __restrict__ st,
-                                                                 float* __restrict__ out) {
+                                                                 float* __restrict__ out, int pos_first,
+                                                                 int qkv_stride, int out_stride) {
     extern __shared__ float sc[];  // T scores then probabilities; then the K and V tiles
     __shared__ float qs[256], ks[256], vs[256];
     __shared__ float red_f[kAttnThreads / kWave];
@@ -154,7 +165,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     __shared__ float inv_s;
     const int head = blockIdx.x;
     const int rep = n_heads / n_kv, g = head / rep;
-    const int pos = st->pos, T = pos + 1;
+    // A decode step: the position in DecodeState.  A prompt chunk: row blockIdx.y of qkv / out
+    // at position pos_first + blockIdx.y (every row's k and v already in the cache).
+    const int pos = pos_first >= 0 ? pos_first + static_cast<int>(blockIdx.y) : st->pos, T = pos + 1;
+    qkv += static_cast<size_t>(blockIdx.y) * qkv_stride;
+    out += static_cast<size_t>(blockIdx.y) * out_stride;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     constexpr int kWaves = kAttnThreads / kWave;
     float* ktile = sc + ((cap + 3) & ~3);   // tile * hd
@@ -322,6 +337,47 @@ size_t attention_lds(int cap, int hd) {
     return (static_cast<size_t>((cap + 3) & ~3) + 2 * static_cast<size_t>(attention_tile(cap, hd)) * hd) * 4;
 }
 
+// Prompt chunk: k = rope(k) and v of rows p < gridDim.y into the cache at pos_first + p, for KV
+// group blockIdx.x -- the values attention_kernel writes for a decode step (same operations),
+// so that every row's attention can read the positions before it from the cache.
+__global__ __launch_bounds__(kAttnThreads) void rope_kv_kernel(const float* __restrict__ qkv, int qkv_stride,
+                                                               const float* __restrict__ cos_tab,
+                                                               const float* __restrict__ sin_tab, int interleaved,
+                                                               float* __restrict__ kc, float* __restrict__ vc,
+                                                               int n_heads, int n_kv, int hd, int cap, int pos_first) {
+    __shared__ float ks[256];
+    const int g = blockIdx.x, p = blockIdx.y, pos = pos_first + p;
+    const float* row = qkv + static_cast<size_t>(p) * qkv_stride;
+    const int d = threadIdx.x;
+    float v0 = 0.0f;
+    if (d < hd) {
+        ks[d] = row[static_cast<size_t>(n_heads + g) * hd + d];
+        v0 = row[static_cast<size_t>(n_heads + n_kv + g) * hd + d];
+    }
+    __syncthreads();
+    rope_head_lds(ks, cos_tab + static_cast<size_t>(pos) * hd, sin_tab + static_cast<size_t>(pos) * hd, hd, interleaved);
+    __syncthreads();
+    if (d < hd) {
+        const size_t at = (static_cast<size_t>(g) * cap + pos) * hd + d;
+        kc[at] = ks[d];
+        vc[at] = v0;
+    }
+}
+
+// Prompt chunk: m[p][n] = silu(gate[p][n]) * up[p][n] from gu rows of 2 ffn values -- gate n and
+// up n at 2n and 2n+1 (interleaved weights) or at n and ffn + n -- the decode step's operations.
+__global__ void silu_mul_rows_kernel(const float* __restrict__ gu, int rows, int ffn, int interleaved,
+                                     float* __restrict__ m) {
+    const long long total = static_cast<long long>(rows) * ffn;
+    for (long long e = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; e < total;
+         e += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const long long p = e / ffn, n = e - p * ffn;
+        const float* r = gu + p * 2 * ffn;
+        const float gate = interleaved ? r[2 * n] : r[n], up = interleaved ? r[2 * n + 1] : r[ffn + n];
+        m[e] = silu_ref(gate) * up;
+    }
+}
+
 // m = silu(g) * u (llama.py:434: sk.silu(gate) * up, two float32 results multiplied), SiLU as
 // the reference's SIMD tables compute it.
 __global__ void silu_mul_kernel(const float* __restrict__ gu, int ffn, float* __restrict__ m) {
@@ -479,6 +535,11 @@ struct Model {
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     Marks marks;
     uint64_t weight_bytes = 0;
+    // prompt chunks (generate): rows per chunk (< 2: one graph step per prompt token) and the
+    // chunk's activations, row-major [rows][width]
+    int prefill_rows = 64;
+    int batch_rows = 0;
+    float *bx = nullptr, *bh = nullptr, *bqkv = nullptr, *battn = nullptr, *bgu = nullptr, *bm = nullptr;
 
     int q_rows() const { return cfg.n_heads * cfg.head_dim; }
     int kv_rows() const { return cfg.n_kv_heads * cfg.head_dim; }
@@ -557,7 +618,7 @@ hipError_t enqueue_step(Model& md, bool with_logits, Marks* mk = nullptr) {
         SMK_MARK(kAttention);
         hipLaunchKernelGGL(attention_kernel, dim3(nh), dim3(kAttnThreads), attention_lds(md.capacity, hd), s,
                            md.qkv, md.cos_tab, md.sin_tab, c.rope_interleaved, kc, vc, nh, nkv, hd, md.capacity,
-                           scale, attention_tile(md.capacity, hd), md.st, md.attn);
+                           scale, attention_tile(md.capacity, hd), md.st, md.attn, -1, 0, 0);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         SMK_MARK(kGemvO);
         if ((e = gemv(L.o, md.attn, md.x, true, s)) != hipSuccess) return e;
@@ -589,6 +650,88 @@ hipError_t enqueue_step(Model& md, bool with_logits, Marks* mk = nullptr) {
     return hipGetLastError();
 }
 #undef SMK_MARK
+
+// The prompt in chunks of rows (examples/llama/llama.py:491-492 runs it token by token): every
+// matrix product takes all rows of the chunk at once (the matrix-core Q4_0 kernel), RMSNorm and
+// SiLU run over the rows, rope_kv_kernel fills the chunk's cache positions, and one attention
+// launch covers (head, row).  Each row's arithmetic is the decode step's, so the cache and the
+// first generated token equal the token-by-token run bit for bit.  Needs quantized matrices (the
+// batched Q4_0 / Q8_0 products equal their one-row calls; the FP32 ones are not pinned to).
+bool chunked_prefill_ok(const Model& md) {
+    return md.prefill_rows >= 2 && (md.cfg.matrix_type == kGgmlQ4_0 || md.cfg.matrix_type == kGgmlQ8_0);
+}
+
+hipError_t batch_buffers(Model& md, int rows) {
+    if (md.batch_rows >= rows) return hipSuccess;
+    for (float** p : {&md.bx, &md.bh, &md.bqkv, &md.battn, &md.bgu, &md.bm}) {
+        if (*p) {
+            md.allocs.erase(std::remove(md.allocs.begin(), md.allocs.end(), static_cast<void*>(*p)), md.allocs.end());
+            (void)hipFree(*p);
+            *p = nullptr;
+        }
+    }
+    md.batch_rows = 0;
+    const smk_llama_config& c = md.cfg;
+    const size_t r = static_cast<size_t>(rows) * 4;
+    const size_t qkv_rows = static_cast<size_t>(md.q_rows() + 2 * md.kv_rows());
+    struct Want { float** p; size_t bytes; };
+    for (const Want& w : {Want{&md.bx, r * c.hidden}, Want{&md.bh, r * c.hidden}, Want{&md.bqkv, r * qkv_rows},
+                          Want{&md.battn, r * md.q_rows()}, Want{&md.bgu, r * 2 * c.ffn}, Want{&md.bm, r * c.ffn}})
+        if (const hipError_t e = dalloc(md, reinterpret_cast<void**>(w.p), w.bytes); e != hipSuccess) return e;
+    md.batch_rows = rows;
+    return hipSuccess;
+}
+
+// Prompt rows [first, first + P): the KV cache at those positions; with logits, also the last
+// row's logits and argmax (DecodeState.pos must then be first + P - 1: the argmax writes
+// tokens[first + P] and advances it).
+hipError_t enqueue_prompt_chunk(Model& md, int first, int P, bool with_logits) {
+    const smk_llama_config& c = md.cfg;
+    hipStream_t s = md.stream;
+    const int nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim, H = c.hidden;
+    const int qkv_rows = md.q_rows() + 2 * md.kv_rows();
+    const int bb = type_block_bytes(c.matrix_type);
+    hipLaunchKernelGGL(embed_rows_kernel, dim3(P), dim3(256), 0, s, md.embed.p, md.embed.type, H, c.vocab,
+                       md.tokens + first, md.bx);
+    if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    const size_t layer_kv = static_cast<size_t>(nkv) * md.capacity * hd;
+    const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(hd)));
+    GemvTuning plain, acc;
+    acc.accumulate = 1;
+    for (int l = 0; l < c.n_layers; ++l) {
+        const Layer& L = md.layers[l];
+        float* kc = md.kc + l * layer_kv;
+        float* vc = md.vc + l * layer_kv;
+        hipError_t e = rms_norm(md.bx, L.attn_norm, md.bh, P, H, c.rms_eps, s);
+        if (e == hipSuccess) e = gemv_quant(bb, P, qkv_rows, H, md.bh, H, L.qkv.p, md.bqkv, qkv_rows, s, &plain);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(rope_kv_kernel, dim3(nkv, P), dim3(kAttnThreads), 0, s, md.bqkv, qkv_rows, md.cos_tab,
+                           md.sin_tab, c.rope_interleaved, kc, vc, nh, nkv, hd, md.capacity, first);
+        hipLaunchKernelGGL(attention_kernel, dim3(nh, P), dim3(kAttnThreads), attention_lds(md.capacity, hd), s,
+                           md.bqkv, md.cos_tab, md.sin_tab, c.rope_interleaved, kc, vc, nh, nkv, hd, md.capacity,
+                           scale, attention_tile(md.capacity, hd), md.st, md.battn, first, qkv_rows, md.q_rows());
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if ((e = gemv_quant(bb, P, H, md.q_rows(), md.battn, md.q_rows(), L.o.p, md.bx, H, s, &acc)) != hipSuccess)
+            return e;
+        if ((e = rms_norm(md.bx, L.ffn_norm, md.bh, P, H, c.rms_eps, s)) != hipSuccess) return e;
+        if ((e = gemv_quant(bb, P, 2 * c.ffn, H, md.bh, H, L.gateup.p, md.bgu, 2 * c.ffn, s, &plain)) != hipSuccess)
+            return e;
+        const long long total = static_cast<long long>(P) * c.ffn;
+        hipLaunchKernelGGL(silu_mul_rows_kernel, dim3(static_cast<int>(std::min<long long>((total + 255) / 256, 4096))),
+                           dim3(256), 0, s, md.bgu, P, c.ffn, md.fuse_silu ? 1 : 0, md.bm);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if ((e = gemv_quant(bb, P, H, c.ffn, md.bm, c.ffn, L.down.p, md.bx, H, s, &acc)) != hipSuccess) return e;
+    }
+    if (!with_logits) return hipSuccess;
+    const float* xl = md.bx + static_cast<size_t>(P - 1) * H;
+    if (const hipError_t e = gemv_normed(md, md.head, xl, md.out_norm, md.h, md.logits, false); e != hipSuccess)
+        return e;
+    hipLaunchKernelGGL(argmax_part_kernel, dim3(kArgmaxParts), dim3(kArgmaxThreads), 0, s, md.logits, c.vocab,
+                       md.part_v, md.part_i);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kWave), 0, s, md.part_v, md.part_i, kArgmaxParts, c.vocab,
+                       md.tokens, md.capacity, md.st);
+    return hipGetLastError();
+}
 
 hipError_t capture(Model& md, bool with_logits, hipGraphExec_t* out) {
     hipError_t e = hipStreamBeginCapture(md.stream, hipStreamCaptureModeThreadLocal);
@@ -880,11 +1023,21 @@ int smk_llama_generate(void* model, const int* prompt, int n_prompt, int n_new, 
         if (prompt[i] < 0 || prompt[i] >= md->cfg.vocab) return fail(SMK_ERR_ARGUMENT, "prompt token out of range");
     if (const int rc = use_device()) return rc;
     SMK_HIP(hipMemcpy(md->tokens, prompt, static_cast<size_t>(n_prompt) * 4, hipMemcpyHostToDevice), "prompt");
-    md->host_pinned[0] = 0;
+    const bool chunked = n_prompt >= 2 && chunked_prefill_ok(*md);
+    if (chunked) SMK_HIP(batch_buffers(*md, std::min(md->prefill_rows, n_prompt)), "prompt chunk buffers");
+    // Chunked: the last prompt row's argmax runs at position n_prompt - 1.
+    md->host_pinned[0] = chunked ? n_prompt - 1 : 0;
     md->host_pinned[1] = n_prompt;
     SMK_HIP(hipMemcpyAsync(md->st, md->host_pinned, sizeof(DecodeState), hipMemcpyHostToDevice, md->stream), "state");
     SMK_HIP(hipEventRecord(md->ev[0], md->stream), "event");
-    for (int i = 0; i < n_prompt; ++i) SMK_HIP(hipGraphLaunch(md->g_logits, md->stream), "prefill graph");
+    if (chunked) {
+        for (int first = 0; first < n_prompt; first += md->batch_rows) {
+            const int P = std::min(md->batch_rows, n_prompt - first);
+            SMK_HIP(enqueue_prompt_chunk(*md, first, P, first + P == n_prompt), "prompt chunk");
+        }
+    } else {
+        for (int i = 0; i < n_prompt; ++i) SMK_HIP(hipGraphLaunch(md->g_logits, md->stream), "prefill graph");
+    }
     SMK_HIP(hipEventRecord(md->ev[1], md->stream), "event");
     for (int i = 0; i < n_new - 1; ++i) SMK_HIP(hipGraphLaunch(md->g_logits, md->stream), "decode graph");
     SMK_HIP(hipEventRecord(md->ev[2], md->stream), "event");
@@ -904,6 +1057,13 @@ int smk_llama_generate(void* model, const int* prompt, int n_prompt, int n_new, 
         seconds[0] = a * 1e-3;
         seconds[1] = b * 1e-3;
     }
+    return ok();
+}
+
+int smk_llama_set_prefill_rows(void* model, int rows) {
+    if (!model) return fail(SMK_ERR_ARGUMENT, "null model");
+    if (rows < 0 || rows > 256) return fail(SMK_ERR_ARGUMENT, "rows must be in [0, 256]");
+    static_cast<Model*>(model)->prefill_rows = rows;
     return ok();
 }
 

@@ -34,10 +34,12 @@
 //   padding of the chunk.  Rows past M hold whatever the buffer held; their products are never
 //   stored.
 //
-// The streaming kernel (K % 1024 == 0, W 16-byte aligned): chunks of 32 blocks.  Per chunk, a
-// wave loads its 16 rows' 576-byte shares of W with coalesced 16-byte loads (9 per lane) and
-// the workgroup loads the chunk's x image (36 KiB at S = 32), one chunk ahead of the
-// arithmetic; both go through two LDS slots, one workgroup barrier per chunk.  The other
+// The streaming kernel (K % 1024 == 0, W 16-byte aligned): chunks of 32 blocks.  Per chunk, the
+// workgroup loads its 64 rows' 576-byte shares of W with coalesced 16-byte loads and the chunk's
+// x image (36 KiB at S = 32), one chunk ahead of the arithmetic; both go through two LDS slots,
+// one workgroup barrier per chunk.  Up to four waves share a 16-row tile, each with its own
+// groups of x rows (measured on MI355X at 14336 x 4096, M = 32: one wave per tile 65 us, two
+// 44 us, four 40 us).  The other
 // kernel (K % 64 == 0) holds the whole x image in LDS and reads W straight from memory with
 // per-lane 4- and 8-byte slices: correct for every such K, but the scattered slices keep it far
 // from the memory roof.
@@ -64,7 +66,6 @@ constexpr int kChunkBlocks = 2 * kChunkPairs;                       // 32 blocks
 constexpr int kWRowBytes = kChunkPairs * 36;                        // a row's share of a chunk
 constexpr int kWRowStride = kWRowBytes + 16;                        // in LDS: rows 148 dwords apart
 constexpr int kWSlotBytes = 16 * kWRowStride;                       // one wave's 16 rows
-constexpr int kWPieces = 16 * kWRowBytes / 16 / kWave;              // 16-byte loads per lane: 9
 constexpr int kWRingBytes = 2 * (kMfmaThreads / kWave) * kWSlotBytes;  // two slots, four waves
 
 // x image chunk bytes (padded to whole 4 KiB rounds of 256 threads x 16 bytes).
@@ -163,11 +164,10 @@ struct PairOps {
     float dx[2][MG];
 };
 
-// x operands of blocks 2p, 2p+1 of an x image chunk (S = 4 MG rows per block).
-template <int MG>
+// x operands of blocks 2p, 2p+1 of an x image chunk (S rows per block), MG groups of 4 rows.
+template <int MG, int S = 4 * MG>
 __device__ __forceinline__ void read_x(const uint8_t* __restrict__ xq_lane, const float* __restrict__ dx_lane, int p,
                                        PairOps<MG>& o) {
-    constexpr int S = 4 * MG;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int b = 2 * p + h;
@@ -215,90 +215,115 @@ __device__ __forceinline__ void store_rows(const float (&acc)[MG][4], int M, int
 
 // ─── streaming kernel ────────────────────────────────────────────────────────
 
-// Rows m < M (M <= 4 MG) of one segment against W rows [16 t, 16 t + 16) for wave t of the grid.
+// Rows m < M (M <= 4 MG) of one segment against W rows [64 blockIdx, 64 blockIdx + 64): four
+// 16-row tiles, SPLIT waves per tile (wave w: tile w % 4, x row groups [(w / 4) MG / SPLIT,
+// (w / 4 + 1) MG / SPLIT)), so that several waves per SIMD hide each other's latencies when M
+// allows.
 // K % 1024 == 0, W 16-byte aligned, N even.  Waves past N run on clamped rows and store nothing
 // (every wave reaches every barrier).
-template <int MG>
-__global__ __launch_bounds__(kMfmaThreads) void gemm_q4_mfma_kernel(int M, int N, int K,
-                                                                    const uint8_t* __restrict__ seg,
-                                                                    const uint8_t* __restrict__ W,
-                                                                    float* __restrict__ y, int ldy, int accumulate) {
-    constexpr int S = 4 * MG;
+template <int MG, int SPLIT>
+__global__ __launch_bounds__(kMfmaThreads * SPLIT) void gemm_q4_mfma_kernel(int M, int N, int K,
+                                                                            const uint8_t* __restrict__ seg,
+                                                                            const uint8_t* __restrict__ W,
+                                                                            float* __restrict__ y, int ldy,
+                                                                            int accumulate) {
+    constexpr int S = 4 * MG, MGW = MG / SPLIT, NT = kMfmaThreads * SPLIT;
     constexpr int XC = x_chunk_bytes(S);
-    constexpr int XP = XC / (16 * kMfmaThreads);  // 16-byte x loads per thread and chunk
+    constexpr int XPC = XC / 16;                        // 16-byte pieces of an x chunk
+    constexpr int WPC = 4 * 16 * kWRowBytes / 16;       // 16-byte pieces of a W chunk (4 tiles)
+    constexpr int XP = (XPC + NT - 1) / NT, WP = (WPC + NT - 1) / NT;
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int tile = wave & 3, mg0 = (wave >> 2) * MGW;
     const int nb = K >> 5, nch = nb / kChunkBlocks;
     const size_t row_bytes = static_cast<size_t>(nb) * 18;
-    const int n0 = (blockIdx.x * (kMfmaThreads / kWave) + wave) * 16;
+    const int nw = blockIdx.x * 64;                     // first W row of the workgroup
     const int g = lane >> 4, i = lane & 15;
 
-    u32x4 wr[kWPieces], xr[XP];
-    // Chunk c into registers: piece q = j * 64 + lane of the wave's 16 rows x 36 pieces.
-    auto load_chunk = [&](int c) {
+    // Chunk c into registers: W piece q = (tile, row, 16-byte column) of 4 x 16 rows x 36.
+    auto load_chunk = [&](int c, u32x4(&wr)[WP], u32x4(&xr)[XP]) {
 #pragma unroll
-        for (int j = 0; j < kWPieces; ++j) {
-            const int q = j * kWave + lane, r = q / 36, col = q - 36 * r;
-            const int row = min(n0 + r, N - 1);
-            wr[j] = *reinterpret_cast<const u32x4*>(W + row * row_bytes + static_cast<size_t>(c) * kWRowBytes + 16 * col);
+        for (int j = 0; j < WP; ++j) {
+            const int q = j * NT + tid;
+            if (WPC % NT == 0 || q < WPC) {
+                const int r = q / 36, col = q - 36 * r;   // r: row of the workgroup's 64
+                const int row = min(nw + r, N - 1);
+                wr[j] = *reinterpret_cast<const u32x4*>(W + row * row_bytes + static_cast<size_t>(c) * kWRowBytes +
+                                                        16 * col);
+            }
         }
-        const uint8_t* xs = seg + static_cast<size_t>(c) * XC;
+        const u32x4* xs = reinterpret_cast<const u32x4*>(seg + static_cast<size_t>(c) * XC);
 #pragma unroll
-        for (int j = 0; j < XP; ++j) xr[j] = reinterpret_cast<const u32x4*>(xs)[j * kMfmaThreads + tid];
+        for (int j = 0; j < XP; ++j) {
+            const int q = j * NT + tid;
+            if (XPC % NT == 0 || q < XPC) xr[j] = xs[q];
+        }
     };
-    auto store_chunk = [&](int slot) {
-        uint8_t* wdst = lds + slot * (kWRingBytes / 2) + wave * kWSlotBytes;
+    auto store_chunk = [&](int slot, const u32x4(&wr)[WP], const u32x4(&xr)[XP]) {
+        uint8_t* wdst = lds + slot * (kWRingBytes / 2);
 #pragma unroll
-        for (int j = 0; j < kWPieces; ++j) {
-            const int q = j * kWave + lane, r = q / 36, col = q - 36 * r;
-            *reinterpret_cast<u32x4*>(wdst + r * kWRowStride + 16 * col) = wr[j];
+        for (int j = 0; j < WP; ++j) {
+            const int q = j * NT + tid;
+            if (WPC % NT == 0 || q < WPC) {
+                const int r = q / 36, col = q - 36 * r;   // tile r / 16, row r % 16 of it
+                *reinterpret_cast<u32x4*>(wdst + (r >> 4) * kWSlotBytes + (r & 15) * kWRowStride + 16 * col) = wr[j];
+            }
         }
         u32x4* xdst = reinterpret_cast<u32x4*>(lds + kWRingBytes + slot * XC);
 #pragma unroll
-        for (int j = 0; j < XP; ++j) xdst[j * kMfmaThreads + tid] = xr[j];
+        for (int j = 0; j < XP; ++j) {
+            const int q = j * NT + tid;
+            if (XPC % NT == 0 || q < XPC) xdst[q] = xr[j];
+        }
     };
 
-    load_chunk(0);
-    store_chunk(0);
-    if (nch > 1) load_chunk(1);
-    lds_barrier();
-
     const bool on = g == (i & 3);
-    float acc[MG][4];
+    float acc[MGW][4];
 #pragma unroll
-    for (int mg = 0; mg < MG; ++mg)
+    for (int mg = 0; mg < MGW; ++mg)
 #pragma unroll
         for (int k = 0; k < 4; ++k) acc[mg][k] = 0.0f;
 
-    for (int c = 0; c < nch; ++c) {
-        const int slot = c & 1;
-        const uint8_t* wrow = lds + slot * (kWRingBytes / 2) + wave * kWSlotBytes + i * kWRowStride;
+    auto compute_chunk = [&](int slot) {
+        const uint8_t* wrow = lds + slot * (kWRingBytes / 2) + tile * kWSlotBytes + i * kWRowStride;
         const uint8_t* xsl = lds + kWRingBytes + slot * XC;
-        const uint8_t* xq_lane = xsl + (i >> 2) * 32 + 8 * g;
-        const float* dx_lane = reinterpret_cast<const float*>(xsl + kChunkBlocks * S * 32) + g;
-        auto read_ops = [&](int p, PairOps<MG>& o) {
+        const uint8_t* xq_lane = xsl + (4 * mg0 + (i >> 2)) * 32 + 8 * g;
+        const float* dx_lane = reinterpret_cast<const float*>(xsl + kChunkBlocks * S * 32) + 4 * mg0 + g;
+        auto read_ops = [&](int p, PairOps<MGW>& o) {
             const uint8_t* wp = wrow + 36 * p;
             o.w[0] = *reinterpret_cast<const uint32_t*>(wp + 4 * g);
             o.w[1] = *reinterpret_cast<const uint32_t*>(wp + 4 * g + 4);
             o.w[2] = *reinterpret_cast<const uint32_t*>(wp + 20 + 4 * g);
             o.w[3] = *reinterpret_cast<const uint32_t*>(wp);
             o.w[4] = *reinterpret_cast<const uint32_t*>(wp + 16);
-            read_x<MG>(xq_lane, dx_lane, p, o);
+            read_x<MGW, S>(xq_lane, dx_lane, p, o);
         };
-        PairOps<MG> cur;
+        PairOps<MGW> cur;
         read_ops(0, cur);
 #pragma unroll 2
         for (int u = 0; u < kChunkPairs; ++u) {
-            PairOps<MG> nxt;
+            PairOps<MGW> nxt;
             read_ops(u + 1 < kChunkPairs ? u + 1 : u, nxt);
-            mfma_pair<MG>(cur, on, acc);
+            mfma_pair<MGW>(cur, on, acc);
             cur = nxt;
         }
-        if (c + 1 < nch) store_chunk(slot ^ 1);  // chunk c + 1 (its loads were issued a chunk ago)
-        if (c + 2 < nch) load_chunk(c + 2);
+    };
+
+    // One chunk in flight: chunk c + 1's loads run during chunk c's arithmetic.  (Two chunks in
+    // flight, in two register sets, measured slower on MI355X at M <= 4.)
+    u32x4 wr[WP], xr[XP];
+    load_chunk(0, wr, xr);
+    store_chunk(0, wr, xr);
+    if (nch > 1) load_chunk(1, wr, xr);
+    lds_barrier();
+    for (int c = 0; c < nch; ++c) {
+        compute_chunk(c & 1);
+        if (c + 1 < nch) store_chunk((c & 1) ^ 1, wr, xr);
+        if (c + 2 < nch) load_chunk(c + 2, wr, xr);
         lds_barrier();
     }
-    store_rows<MG>(acc, M, N, n0 + i, g, y, ldy, accumulate);
+    store_rows<MGW>(acc, M - 4 * mg0, N, nw + 16 * tile + i, g, y + static_cast<size_t>(4 * mg0) * ldy, ldy,
+                    accumulate);
 }
 
 // ─── whole-image kernel (any K % 64 == 0) ────────────────────────────────────
@@ -390,14 +415,14 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_q4_mfma_whole_kernel(int M,
     store_rows<MG>(acc, M, N, n0 + i, g, y, ldy, accumulate);
 }
 
-template <int MG>
+template <int MG, int SPLIT>
 hipError_t launch_streaming(int M, int N, int K, const uint8_t* seg, const uint8_t* W, float* y, int ldy, int acc,
                             hipStream_t stream) {
-    auto kernel = gemm_q4_mfma_kernel<MG>;
+    auto kernel = gemm_q4_mfma_kernel<MG, SPLIT>;
     const size_t lds = kWRingBytes + 2 * static_cast<size_t>(x_chunk_bytes(4 * MG));
     if (const hipError_t e = allow_lds(kernel, lds); e != hipSuccess) return e;
-    const int grid = ((N + 15) / 16 + 3) / 4;
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kMfmaThreads), lds, stream, M, N, K, seg, W, y, ldy, acc);
+    const int grid = (N + 63) / 64;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kMfmaThreads * SPLIT), lds, stream, M, N, K, seg, W, y, ldy, acc);
     return hipGetLastError();
 }
 
@@ -479,10 +504,10 @@ hipError_t gemm_q4_mfma(int M, int N, int K, const float* x, int ldx, const uint
         hipError_t e;
         if (L.streaming) {
             switch (L.rows) {
-                case 4: e = launch_streaming<1>(mr, N, K, seg, W, ym, ldy, acc, stream); break;
-                case 8: e = launch_streaming<2>(mr, N, K, seg, W, ym, ldy, acc, stream); break;
-                case 16: e = launch_streaming<4>(mr, N, K, seg, W, ym, ldy, acc, stream); break;
-                default: e = launch_streaming<8>(mr, N, K, seg, W, ym, ldy, acc, stream); break;
+                case 4: e = launch_streaming<1, 1>(mr, N, K, seg, W, ym, ldy, acc, stream); break;
+                case 8: e = launch_streaming<2, 2>(mr, N, K, seg, W, ym, ldy, acc, stream); break;
+                case 16: e = launch_streaming<4, 4>(mr, N, K, seg, W, ym, ldy, acc, stream); break;
+                default: e = launch_streaming<8, 4>(mr, N, K, seg, W, ym, ldy, acc, stream); break;
             }
         } else {
             switch (L.rows) {

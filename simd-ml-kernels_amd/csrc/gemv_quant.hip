@@ -42,11 +42,11 @@ typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr int kThreads = 256;
 // Rows of x from which a Q4_0 product takes the matrix-core kernel.  Measured on MI355X
-// (graph-replayed, us, matrix-core / 8-row GEMV launches): 14336x4096 M=2 19.7/20.0, M=4
-// 19.7/31.4, M=8 26.5/57.3, M=32 65/229; 8192x2048 M=2 11.9/9.3, M=4 12.1/13.6; 2048x8192
-// (128 row tiles for 256 CUs) M=4 30.6/28.6, M=8 43.6/192.
-constexpr int kMfmaMinRows = 4;
-inline bool mfma_rows_pay(int M, int N) { return M > 4 || (M == 4 && N >= 4096); }
+// (graph-replayed, us, matrix-core / 8-row GEMV launches): 14336x4096 M=2 20.0/20.0, M=3
+// 20.0/25.5, M=4 17.9/31.4, M=8 21.2/57.3, M=32 40.2/229; 8192x2048 M=2 ~11/9.3, M=4
+// 11.2/13.6, M=32 23.7/83.3; 2048x8192 (128 row tiles for 256 CUs) M=4 30.3/28.6, M=8 33.0/193.
+constexpr int kMfmaMinRows = 3;
+inline bool mfma_rows_pay(int M, int N) { return M > 4 || N >= 4096; }
 
 // ─── x -> Q8 quants in LDS ───────────────────────────────────────────────────
 

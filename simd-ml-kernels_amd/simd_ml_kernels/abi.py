@@ -79,6 +79,7 @@ SIGNATURES = {
     "smk_llama_generate": [_p, _p, _i, _i, _p, _p],
     "smk_llama_info": [_p, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(ctypes.c_ulonglong)],
     "smk_llama_step_profile": [_p, _i, _p, _p, _i],
+    "smk_llama_set_prefill_rows": [_p, _i],
     "smk_malloc": [ctypes.POINTER(_p), _sz],
     "smk_free": [_p],
     "smk_memcpy_h2d": [_p, _p, _sz],

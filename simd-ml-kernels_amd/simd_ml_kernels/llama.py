@@ -350,10 +350,12 @@ class Llama:
 
     def generate(self, prompt_ids: Sequence[int], max_new_tokens: int, stats: dict | None = None,
                  stop_at_eos: bool = True) -> Iterator[int]:
-        """Greedy decode (llama.py:481-505): prefill the prompt one token at a time, then yield up
-        to max_new_tokens ids, stopping after an EOS id unless stop_at_eos is False.  On the device
-        path the whole run is one engine call (argmax on the GPU, tokens copied back at the end):
-        tokens after an EOS never change those before it, so stopping is a truncation."""
+        """Greedy decode (llama.py:481-505): prefill the prompt, then yield up to max_new_tokens
+        ids, stopping after an EOS id unless stop_at_eos is False.  On the device path the whole
+        run is one engine call (argmax on the GPU, tokens copied back at the end): tokens after an
+        EOS never change those before it, so stopping is a truncation.  The device path prefills
+        quantized models in chunks of prompt rows (set_prefill_rows), the reference's loop one
+        token at a time; the cache and the tokens are the same bit for bit."""
         prompt = [int(t) for t in prompt_ids]
         if max_new_tokens <= 0:
             return
@@ -386,6 +388,11 @@ class Llama:
             if stats is not None:
                 stats["decode_s"] += time.perf_counter() - t
                 stats["decode_steps"] += 1
+
+    def set_prefill_rows(self, rows: int) -> None:
+        """Device path: prompt rows per prefill chunk (0 or 1: one decode step per prompt token)."""
+        if self._engine is not None:
+            self._engine.set_prefill_rows(int(rows))
 
     def close(self) -> None:
         if self._engine is not None:
@@ -469,6 +476,9 @@ class _Engine:
         prof["total"] = prof.get("total", 0.0) + float(ms.sum()) * 1e-3
         prof["steps"] = prof.get("steps", 0) + 1
         return out
+
+    def set_prefill_rows(self, rows: int) -> None:
+        abi.check(self.L.smk_llama_set_prefill_rows(self.h, rows), "smk_llama_set_prefill_rows")
 
     def generate(self, prompt: list[int], n_new: int) -> tuple[np.ndarray, float, float]:
         p = np.asarray(prompt, np.int32)

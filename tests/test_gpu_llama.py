@@ -112,6 +112,29 @@ def test_mid_model_logits_equal_reference_loop(tmp_path):
         m.close()
 
 
+@pytest.mark.parametrize("wname,model,rows", [("q4_0", "tiny", 64), ("q4_0", "tiny", 3), ("q8_0", "tiny", 5),
+                                              ("q4_0", "mid", 4), ("q4_0", "mid", 64)])
+def test_chunked_prefill_equals_token_by_token(tmp_path, wname, model, rows):
+    """The prompt in chunks of rows (matrix-core products over the rows, one attention launch per
+    chunk) leaves the same KV cache and first token as one decode step per prompt token: the
+    generated tokens match, and so does every bit of a further step's logits, which read the
+    whole cache."""
+    cfg = TINY if model == "tiny" else MID
+    gtype, _ = WTYPES[wname]
+    path, prompt = llama.write_synthetic_model(str(tmp_path), cfg, seed=31, n_prompt=11, weight_type=gtype)
+    m = llama.Llama(str(tmp_path), gguf=path)
+    try:
+        out = {}
+        for r in (0, rows):
+            m.set_prefill_rows(r)
+            ids = list(m.generate(prompt, 6, stop_at_eos=False))
+            out[r] = (ids, m.step(ids[-1]))
+        assert out[0][0] == out[rows][0]
+        np.testing.assert_array_equal(out[0][1].view(np.uint32), out[rows][1].view(np.uint32))
+    finally:
+        m.close()
+
+
 def test_tiny_module_loop_matches_engine(tmp_path):
     path, prompt, _ = _tiny(tmp_path, "q4_0", seed=22)
     eng = llama.Llama(str(tmp_path), gguf=path)
