@@ -215,6 +215,7 @@ __device__ __forceinline__ void store_rows(const float (&acc)[MG][4], int M, int
 
 // ─── streaming kernel ────────────────────────────────────────────────────────
 
+// LDS: two x slots of x_chunk_bytes(S), then (at w_ring = their size) two W slots of four tiles.
 // Rows m < M (M <= 4 MG) of one segment against W rows [64 blockIdx, 64 blockIdx + 64): four
 // 16-row tiles, SPLIT waves per tile (wave w: tile w % 4, x row groups [(w / 4) MG / SPLIT,
 // (w / 4 + 1) MG / SPLIT)), so that several waves per SIMD hide each other's latencies when M
@@ -226,7 +227,7 @@ __global__ __launch_bounds__(kMfmaThreads * SPLIT) void gemm_q4_mfma_kernel(int 
                                                                             const uint8_t* __restrict__ seg,
                                                                             const uint8_t* __restrict__ W,
                                                                             float* __restrict__ y, int ldy,
-                                                                            int accumulate) {
+                                                                            int accumulate, int w_ring) {
     constexpr int S = 4 * MG, MGW = MG / SPLIT, NT = kMfmaThreads * SPLIT;
     constexpr int XC = x_chunk_bytes(S);
     constexpr int XPC = XC / 16;                        // 16-byte pieces of an x chunk
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(kMfmaThreads * SPLIT) void gemm_q4_mfma_kernel(int 
         }
     };
     auto store_chunk = [&](int slot, const u32x4(&wr)[WP], const u32x4(&xr)[XP]) {
-        uint8_t* wdst = lds + slot * (kWRingBytes / 2);
+        uint8_t* wdst = lds + w_ring + slot * (kWRingBytes / 2);
 #pragma unroll
         for (int j = 0; j < WP; ++j) {
             const int q = j * NT + tid;
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(kMfmaThreads * SPLIT) void gemm_q4_mfma_kernel(int 
                 *reinterpret_cast<u32x4*>(wdst + (r >> 4) * kWSlotBytes + (r & 15) * kWRowStride + 16 * col) = wr[j];
             }
         }
-        u32x4* xdst = reinterpret_cast<u32x4*>(lds + kWRingBytes + slot * XC);
+        u32x4* xdst = reinterpret_cast<u32x4*>(lds + slot * XC);
 #pragma unroll
         for (int j = 0; j < XP; ++j) {
             const int q = j * NT + tid;
@@ -285,8 +286,11 @@ __global__ __launch_bounds__(kMfmaThreads * SPLIT) void gemm_q4_mfma_kernel(int 
         for (int k = 0; k < 4; ++k) acc[mg][k] = 0.0f;
 
     auto compute_chunk = [&](int slot) {
-        const uint8_t* wrow = lds + slot * (kWRingBytes / 2) + tile * kWSlotBytes + i * kWRowStride;
-        const uint8_t* xsl = lds + kWRingBytes + slot * XC;
+        // Every LDS read of a chunk is a per-lane base plus an offset below 64 KiB (the LDS
+        // instructions' immediate): the x ring comes first, and the W ring's offset (2 XC) is a
+        // kernel argument, so that the compiler cannot fold it into the immediates.
+        const uint8_t* wrow = lds + w_ring + slot * (kWRingBytes / 2) + tile * kWSlotBytes + i * kWRowStride;
+        const uint8_t* xsl = lds + slot * XC;
         const uint8_t* xq_lane = xsl + (4 * mg0 + (i >> 2)) * 32 + 8 * g;
         const float* dx_lane = reinterpret_cast<const float*>(xsl + kChunkBlocks * S * 32) + 4 * mg0 + g;
         auto read_ops = [&](int p, PairOps<MGW>& o) {
@@ -422,7 +426,9 @@ hipError_t launch_streaming(int M, int N, int K, const uint8_t* seg, const uint8
     const size_t lds = kWRingBytes + 2 * static_cast<size_t>(x_chunk_bytes(4 * MG));
     if (const hipError_t e = allow_lds(kernel, lds); e != hipSuccess) return e;
     const int grid = (N + 63) / 64;
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kMfmaThreads * SPLIT), lds, stream, M, N, K, seg, W, y, ldy, acc);
+    const int w_ring = 2 * x_chunk_bytes(4 * MG);  // the W ring follows the two x slots
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kMfmaThreads * SPLIT), lds, stream, M, N, K, seg, W, y, ldy, acc,
+                       w_ring);
     return hipGetLastError();
 }
 
