@@ -841,7 +841,8 @@ int smk_llama_create(const smk_llama_config* cfg, void** model) {
     if (md->tied) md->head = md->embed;
     {
         const int depth = uniform_depth(c.hidden);
-        md->fuse_norm = c.matrix_type == kGgmlQ4_0 && c.hidden <= 8192 && c.hidden % 64 == 0 && depth >= 0 &&
+        md->fuse_norm = c.matrix_type == kGgmlQ4_0 && c.hidden <= 8192 && c.hidden % 64 == 0 &&
+                        uniform_equal_leaves(c.hidden, depth) &&
                         (8 << depth) <= 1024 && (md->q_rows() + 2 * md->kv_rows()) % 2 == 0 && c.vocab % 2 == 0;
         md->fuse_silu = c.matrix_type == kGgmlQ4_0 && c.hidden % 64 == 0;
     }

@@ -459,6 +459,7 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
         float4 xr[4], wr[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
+            if (u * NT >= quads) break;  // uniform: no thread has a quad this far (no idle loads)
             const int qd = static_cast<int>(threadIdx.x) + u * NT;
             const int c = qd < quads ? qd : 0;
             xr[u] = x4[c];
@@ -466,15 +467,23 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
         }
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_sched_barrier(0);
+        // Every wave issues its x loads before any wave issues weight loads: a CU's vector loads
+        // come back in the order they were issued, and x queued behind other waves' weight loads
+        // arrived with the weights (measured in the decode step: ~2900 cycles later).
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
         load_group(0, wa);
         __builtin_amdgcn_sched_barrier(0);
+        // x into LDS with 8 spare floats after every leaf of the pairwise tree (leaves of
+        // K >> depth values: the host checks they are equal), read back conflict-free by the sum.
+        const int leaf = K >> norm_depth;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int qd = static_cast<int>(threadIdx.x) + u * NT;
-            if (qd < quads) reinterpret_cast<float4*>(xf)[qd] = xr[u];
+            if (qd < quads) reinterpret_cast<float4*>(xf + 8 * ((4 * qd) / leaf))[qd] = xr[u];
         }
         lds_barrier();
-        const float total = uniform_chunk_sum<NT>(xf, K, norm_depth, wave_sum);
+        const float total = uniform_chunk_sum<NT>(xf, K, norm_depth, wave_sum, 8);
         const float var = static_cast<float>(static_cast<double>(total) / static_cast<double>(K));
         const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(var) + norm_eps));
 #pragma unroll
@@ -886,7 +895,7 @@ hipError_t launch_ordered_ch(int M, int N, int K, const float* x, int ldx, const
     if (nrm.w && (M != 1 || (8 << nrm.depth) > NT)) return hipErrorInvalidValue;
     if (nrm.silu_pairs && (LPR > 32 || (rows_per_wg & 1) || accumulate_unsupported(acc))) return hipErrorInvalidValue;
     if (rows_per_wg <= 0) rows_per_wg = std::max(kRows, (N + 511) / 512);
-    const size_t extra = nrm.w ? static_cast<size_t>(K) * 4 : 0;
+    const size_t extra = nrm.w ? (static_cast<size_t>(K) + (8u << nrm.depth)) * 4 : 0;
     // Two phase-1 buffers (phase 2 of a group overlaps the next group's phase 1) when a
     // workgroup has several groups and they fit.
     const int nbuf = (rows_per_wg > kRows && ordered_lds_bytes(M, K, kRows, 2) + extra <= 150 * 1024) ? 2 : 1;
@@ -945,11 +954,13 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
         nrm.silu_pairs = 1;
     }
     if (t && t->norm_w) {
-        // Fused RMSNorm: one row of x, K <= 8192, the pair kernel (even N), a uniform tree.
+        // Fused RMSNorm: one row of x, K <= 8192, the pair kernel (even N), a uniform tree of
+        // equal leaves.
         nrm.w = t->norm_w;
         nrm.eps = t->norm_eps;
         nrm.depth = uniform_depth(K);
-        if (M != 1 || K > 8192 || nrm.depth < 0 || generic || (N & 1) || (8 << nrm.depth) > 1024 ||
+        if (M != 1 || K > 8192 || !uniform_equal_leaves(K, nrm.depth) || generic || (N & 1) ||
+            (8 << nrm.depth) > 1024 ||
             reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(t->norm_w) % 16)
             return hipErrorInvalidValue;
     }
@@ -993,7 +1004,7 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
             if (lpr > 32) lpr = 32;    // two rows at least side by side in a wave
         }
         int nt = (t && t->threads) ? t->threads : 256;
-        const size_t cap = kLdsCap - (nrm.w ? static_cast<size_t>(K) * 4 : 0);
+        const size_t cap = kLdsCap - (nrm.w ? (static_cast<size_t>(K) + (8u << nrm.depth)) * 4 : 0);
         if (!(t && t->threads)) {
             while (nt < 1024 && nt < rpw * lpr) nt *= 2;
             while (nt > 256 && ordered_lds_bytes(1, K, nt / lpr) > cap) nt /= 2;

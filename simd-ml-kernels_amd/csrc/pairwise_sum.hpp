@@ -28,8 +28,13 @@ __device__ __forceinline__ void leaf_of(int l, int depth, int n, int& start, int
     }
 }
 
+// pad: leaf l's values start `pad * l` floats after their place in q (a caller that stores the
+// chunk with 8 spare floats per leaf makes the eight lanes of the leaves of one wave read eight
+// different groups of LDS banks; with leaves of a multiple of 64 values and no padding they all
+// read the same eight banks).
 template <int kThreads>
-__device__ __forceinline__ float uniform_chunk_sum(const float* __restrict__ q, int n, int depth, float* wave_sum) {
+__device__ __forceinline__ float uniform_chunk_sum(const float* __restrict__ q, int n, int depth, float* wave_sum,
+                                                   int pad = 0) {
     constexpr int kWaves = kThreads / kWave;
     const int leaves = 1 << depth;
     const int l = threadIdx.x >> 3, k = threadIdx.x & 7;
@@ -38,13 +43,18 @@ __device__ __forceinline__ float uniform_chunk_sum(const float* __restrict__ q, 
     if (l < leaves) {
         leaf_of(l, depth, n, start, len);
         const int full = len - (len % 8);
-        // Leaves hold at most 128 values (16 per lane): every read is issued before the sums.
+        q += pad * l;
+        // Leaves hold at most 128 values (16 per lane): every read is issued before the sums,
+        // unconditionally (a read past the leaf's full groups re-reads its first value and is
+        // dropped), so that the reads are not serialized by a wait each.
         float v[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             const int i = 8 * j + k;
-            v[j] = i < full ? q[start + i] : 0.0f;
+            v[j] = q[start + (i < full ? i : 0)];
         }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = 8 * j + k < full ? v[j] : 0.0f;
         r = v[0] * v[0];
 #pragma unroll
         for (int j = 1; j < 16; ++j)
@@ -89,6 +99,12 @@ inline int uniform_depth(int len) {
     n2 -= n2 % 8;
     const int a = uniform_depth(n2), b = uniform_depth(len - n2);
     return (a >= 0 && a == b) ? a + 1 : -1;
+}
+
+// The uniform tree of len values splits every node into exact halves (leaves of len >> depth
+// values): every split point len / 2 at each level is a multiple of 8.
+inline bool uniform_equal_leaves(int len, int depth) {
+    return depth >= 0 && (depth == 0 || len % (1 << (depth + 3)) == 0);
 }
 
 }  // namespace smk
