@@ -219,23 +219,26 @@ __device__ __forceinline__ void store_rows(const float (&acc)[MG][4], int M, int
 // Rows m < M (M <= 4 MG) of one segment against W rows [64 blockIdx, 64 blockIdx + 64): four
 // 16-row tiles, SPLIT waves per tile (wave w: tile w % 4, x row groups [(w / 4) MG / SPLIT,
 // (w / 4 + 1) MG / SPLIT)), so that several waves per SIMD hide each other's latencies when M
-// allows.
+// allows.  With few rows of W (fewer workgroups than CUs) the grid's y dimension splits the x
+// row groups further: workgroup (t, u) takes groups [u MG / YS, (u + 1) MG / YS) of W rows
+// [64 t, 64 t + 64), reading those rows of W once per u (from the caches after the first).
 // K % 1024 == 0, W 16-byte aligned, N even.  Waves past N run on clamped rows and store nothing
 // (every wave reaches every barrier).
-template <int MG, int SPLIT>
+template <int MG, int SPLIT, int YS>
 __global__ __launch_bounds__(kMfmaThreads * SPLIT) void gemm_q4_mfma_kernel(int M, int N, int K,
                                                                             const uint8_t* __restrict__ seg,
                                                                             const uint8_t* __restrict__ W,
                                                                             float* __restrict__ y, int ldy,
                                                                             int accumulate, int w_ring) {
-    constexpr int S = 4 * MG, MGW = MG / SPLIT, NT = kMfmaThreads * SPLIT;
+    constexpr int S = 4 * MG, MGW = MG / (SPLIT * YS), NT = kMfmaThreads * SPLIT;
+    static_assert(MGW * SPLIT * YS == MG, "x row groups split evenly over waves and grid rows");
     constexpr int XC = x_chunk_bytes(S);
     constexpr int XPC = XC / 16;                        // 16-byte pieces of an x chunk
     constexpr int WPC = 4 * 16 * kWRowBytes / 16;       // 16-byte pieces of a W chunk (4 tiles)
     constexpr int XP = (XPC + NT - 1) / NT, WP = (WPC + NT - 1) / NT;
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const int tile = wave & 3, mg0 = (wave >> 2) * MGW;
+    const int tile = wave & 3, mg0 = (static_cast<int>(blockIdx.y) * SPLIT + (wave >> 2)) * MGW;
     const int nb = K >> 5, nch = nb / kChunkBlocks;
     const size_t row_bytes = static_cast<size_t>(nb) * 18;
     const int nw = blockIdx.x * 64;                     // first W row of the workgroup
@@ -419,15 +422,15 @@ __global__ __launch_bounds__(kMfmaThreads) void gemm_q4_mfma_whole_kernel(int M,
     store_rows<MG>(acc, M, N, n0 + i, g, y, ldy, accumulate);
 }
 
-template <int MG, int SPLIT>
+template <int MG, int SPLIT, int YS>
 hipError_t launch_streaming(int M, int N, int K, const uint8_t* seg, const uint8_t* W, float* y, int ldy, int acc,
                             hipStream_t stream) {
-    auto kernel = gemm_q4_mfma_kernel<MG, SPLIT>;
+    auto kernel = gemm_q4_mfma_kernel<MG, SPLIT, YS>;
     const size_t lds = kWRingBytes + 2 * static_cast<size_t>(x_chunk_bytes(4 * MG));
     if (const hipError_t e = allow_lds(kernel, lds); e != hipSuccess) return e;
     const int grid = (N + 63) / 64;
     const int w_ring = 2 * x_chunk_bytes(4 * MG);  // the W ring follows the two x slots
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kMfmaThreads * SPLIT), lds, stream, M, N, K, seg, W, y, ldy, acc,
+    hipLaunchKernelGGL(kernel, dim3(grid, YS), dim3(kMfmaThreads * SPLIT), lds, stream, M, N, K, seg, W, y, ldy, acc,
                        w_ring);
     return hipGetLastError();
 }
@@ -503,6 +506,13 @@ hipError_t gemm_q4_mfma(int M, int N, int K, const float* x, int ldx, const uint
                            static_cast<long long>(L.dx_off));
         if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
+    // Grid rows of the streaming kernel: split the x row groups while the workgroups of 64 W rows
+    // leave CUs idle (at most 256 workgroups; one group of 4 x rows per wave at the finest).
+    int ys = 1;
+    {
+        const int gx = (N + 63) / 64;
+        while (2 * ys <= L.rows / 4 && 2 * ys <= 8 && gx * 2 * ys <= 256) ys *= 2;
+    }
     for (int m0 = 0; m0 < M; m0 += L.rows) {
         const int mr = std::min(L.rows, M - m0);
         const uint8_t* seg = ws + static_cast<size_t>(m0 / L.rows) * L.seg_bytes;
@@ -510,10 +520,21 @@ hipError_t gemm_q4_mfma(int M, int N, int K, const float* x, int ldx, const uint
         hipError_t e;
         if (L.streaming) {
             switch (L.rows) {
-                case 4: e = launch_streaming<1, 1>(mr, N, K, seg, W, ym, ldy, acc, stream); break;
-                case 8: e = launch_streaming<2, 2>(mr, N, K, seg, W, ym, ldy, acc, stream); break;
-                case 16: e = launch_streaming<4, 4>(mr, N, K, seg, W, ym, ldy, acc, stream); break;
-                default: e = launch_streaming<8, 4>(mr, N, K, seg, W, ym, ldy, acc, stream); break;
+                case 4: e = launch_streaming<1, 1, 1>(mr, N, K, seg, W, ym, ldy, acc, stream); break;
+                case 8: e = ys == 1 ? launch_streaming<2, 2, 1>(mr, N, K, seg, W, ym, ldy, acc, stream)
+                                    : launch_streaming<2, 1, 2>(mr, N, K, seg, W, ym, ldy, acc, stream);
+                    break;
+                case 16:
+                    e = ys == 1   ? launch_streaming<4, 4, 1>(mr, N, K, seg, W, ym, ldy, acc, stream)
+                        : ys == 2 ? launch_streaming<4, 2, 2>(mr, N, K, seg, W, ym, ldy, acc, stream)
+                                  : launch_streaming<4, 1, 4>(mr, N, K, seg, W, ym, ldy, acc, stream);
+                    break;
+                default:
+                    e = ys == 1   ? launch_streaming<8, 4, 1>(mr, N, K, seg, W, ym, ldy, acc, stream)
+                        : ys == 2 ? launch_streaming<8, 4, 2>(mr, N, K, seg, W, ym, ldy, acc, stream)
+                        : ys == 4 ? launch_streaming<8, 2, 4>(mr, N, K, seg, W, ym, ldy, acc, stream)
+                                  : launch_streaming<8, 1, 8>(mr, N, K, seg, W, ym, ldy, acc, stream);
+                    break;
             }
         } else {
             switch (L.rows) {
