@@ -39,6 +39,7 @@ namespace smk {
 namespace {
 
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef float f32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr int kThreads = 256;
 // Rows of x from which a Q4_0 product takes the matrix-core kernel.  Measured on MI355X
@@ -94,43 +95,51 @@ __device__ __forceinline__ void quantize_quad(const float (&v)[4], int m, int kq
 // The first PQ quads a thread quantizes are loaded into registers before the kernel issues
 // its weight loads, so that waiting for x does not wait for W (global loads retire in
 // order); quads past PQ * NT (very long rows) are loaded and quantized afterwards.
-template <int NT, int PQ>
+template <int NT, int PQ, int MT>
 struct XPreload {
     float v[PQ][4];
-    // Unconditional loads (an index past the end reloads quad 0): the wait for x then has
-    // a known count of younger loads and does not wait for the weights issued after it.
+    // A wave loads pass p only when one of its lanes has a quad there (waves past the end of
+    // x neither load nor quantize, and leave the SIMD to those that do).  Within a loading
+    // wave the loads are unconditional (an index past the end reloads quad 0), so the wait
+    // for x has a known count of younger loads and does not wait for the weights issued
+    // after it.  The loads sit in blocks of their own, ahead of the weight loads: a load in
+    // the same block as a wave-uniform branch to its only use is moved into that branch by
+    // the compiler, behind the weights.
+    __device__ __forceinline__ static bool wave_has(int p, int total) {
+        return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) & ~(kWave - 1)) + p * NT < total;
+    }
     __device__ __forceinline__ void load(const float* __restrict__ x, int ldx, int M, int K) {
         const int quads = K >> 2, total = M * quads;
 #pragma unroll
         for (int p = 0; p < PQ; ++p) {
+            if (!wave_has(p, total)) break;
             int qd = static_cast<int>(threadIdx.x) + p * NT;
             qd = qd < total ? qd : 0;
-            const int m = qd / quads, kq = qd - m * quads;
-            const float* src = x + static_cast<size_t>(m) * ldx + 4 * kq;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[p][i] = src[i];
+            const int m = MT == 1 ? 0 : qd / quads, kq = qd - m * quads;
+            const f32x4a4 t = *reinterpret_cast<const f32x4a4*>(x + static_cast<size_t>(m) * ldx + 4 * kq);
+            v[p][0] = t.x;
+            v[p][1] = t.y;
+            v[p][2] = t.z;
+            v[p][3] = t.w;
         }
     }
     template <bool kPlanes, bool kBias, bool kChainBias = false>
     __device__ __forceinline__ void quantize(const float* __restrict__ x, int ldx, int M, int K, uint32_t* lds_q,
                                              int* lds_bias, float* lds_dx, int* bad) {
         const int quads = K >> 2, total = M * quads;
-        // Every preloaded quad is processed (a quad past the end recomputes quad 0 and stores
-        // nothing), so no x value is consumed under a branch the compiler could sink its load
-        // into, past the weight loads.
 #pragma unroll
         for (int p = 0; p < PQ; ++p) {
-            if (p * NT >= total) break;  // uniform: no thread has a quad this far
+            if (!wave_has(p, total)) break;
             const int qd = static_cast<int>(threadIdx.x) + p * NT;
             const bool live = qd < total;
-            const int qe = live ? qd : 0, m = qe / quads;
+            const int qe = live ? qd : 0, m = MT == 1 ? 0 : qe / quads;
             quantize_quad<kPlanes, kBias, kChainBias>(v[p], m, qe - m * quads, K, lds_q, lds_bias, lds_dx, bad, live);
         }
         for (int qd = static_cast<int>(threadIdx.x) + PQ * NT; qd < total; qd += NT) {
-            const int m = qd / quads, kq = qd - m * quads;
-            const float* src = x + static_cast<size_t>(m) * ldx + 4 * kq;
-            const float t[4] = {src[0], src[1], src[2], src[3]};
-            quantize_quad<kPlanes, kBias, kChainBias>(t, m, kq, K, lds_q, lds_bias, lds_dx, bad);
+            const int m = MT == 1 ? 0 : qd / quads, kq = qd - m * quads;
+            const f32x4a4 t = *reinterpret_cast<const f32x4a4*>(x + static_cast<size_t>(m) * ldx + 4 * kq);
+            const float u[4] = {t.x, t.y, t.z, t.w};
+            quantize_quad<kPlanes, kBias, kChainBias>(u, m, kq, K, lds_q, lds_bias, lds_dx, bad);
         }
     }
 };
@@ -287,11 +296,15 @@ __global__ __launch_bounds__(NT) void gemv_pairs_kernel(int M, int N, int K, con
     };
 
     // x first, then the first weight step: the x-quant below waits only for x.
-    XPreload<NT, PQ> xp;
+    XPreload<NT, PQ, MT> xp;
     xp.load(x, ldx, M, K);
     // Keep every x load ahead of the weight loads: a compiler-only fence (no instruction)
     // for the IR passes and a scheduling barrier for the machine scheduler.
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_sched_barrier(0);
+    // Every wave issues its x loads before any wave issues weight loads: a CU returns vector
+    // loads in issue order, and x queued behind other waves' weights arrived with them.
+    __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     uint32_t wa[U][D], wb[U][D];
     load_step(0, wa);  // steps >= 1: K/32 >= 2 and every workgroup owns at least one row
@@ -497,9 +510,11 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
         }
         lds_barrier();
     } else {
-        XPreload<NT, PQ> xp;
+        XPreload<NT, PQ, MT> xp;
         xp.load(x, ldx, M, K);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();  // every wave's x loads ahead of all weight loads, as above
         __builtin_amdgcn_sched_barrier(0);
         load_group(0, wa);
         __builtin_amdgcn_sched_barrier(0);
