@@ -573,6 +573,7 @@ hipError_t gemv_normed(const Model& md, const Mat& W, const float* x, const floa
     GemvTuning t;
     t.accumulate = accumulate ? 1 : 0;
     t.silu_pairs = silu_pairs ? 1 : 0;
+    t.stream_weights = 1;
     if (md.fuse_norm && W.type == kGgmlQ4_0) {
         t.norm_w = nw;
         t.norm_eps = md.cfg.rms_eps;
@@ -588,6 +589,7 @@ hipError_t gemv(const Mat& W, const float* x, float* y, bool accumulate, hipStre
         return gemm_tb(0, 1, W.rows, W.cols, 1.0f, x, W.cols, W.p, W.cols, accumulate ? 1.0f : 0.0f, y, W.rows, s);
     GemvTuning t;
     t.accumulate = accumulate ? 1 : 0;
+    t.stream_weights = 1;
     return gemv_quant(type_block_bytes(W.type), 1, W.rows, W.cols, x, W.cols, W.p, y, W.rows, s, &t);
 }
 

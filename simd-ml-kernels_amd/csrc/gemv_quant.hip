@@ -34,6 +34,8 @@
 #include "pairwise_sum.hpp"
 
 #include <algorithm>
+#include <cstdlib>
+#include <type_traits>
 
 namespace smk {
 namespace {
@@ -410,7 +412,15 @@ __device__ __forceinline__ void wave_lds_sync() {
 // w * (x * float(1 / sqrt(mean(x*x) + eps))) (llama.py:184-187, the pairwise mean of squares
 // as the RMSNorm kernel computes it; norm_depth is the depth of its uniform tree), bit for bit
 // what the separate kernel would hand over.
-template <int LPR, int MT, int NT, int CH>
+// kStream (one row of x, CH <= 2, the G rows of a wave a multiple of 16 bytes, W 16-byte
+// aligned): each wave streams the contiguous bytes of its own G rows with coalesced 16-byte
+// non-temporal loads (every 128-byte line is read by one instruction, so nothing needs the
+// vector L1 between loads), stages them in its own LDS region, and its lanes read their pairs
+// from there; without it, a lane loads its 36-byte pairs itself (three loads that touch the
+// same lines, cached).
+// kNorm: norm_w is set (the fused RMSNorm prologue; a kernel of its own, so that the wait
+// counts of the plain prologue are not merged with this one's).
+template <int LPR, int MT, int NT, int CH, int kStream, bool kNorm>
 __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K, const float* __restrict__ x,
                                                              int ldx, const uint8_t* __restrict__ W,
                                                              float* __restrict__ y, int ldy, int rows_per_wg,
@@ -424,7 +434,12 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
     constexpr int kChains = 4 * kRows * MT;  // reference lanes of a group (phase 2), at most
     constexpr int P2 = (kChains + kWave - 1) / kWave;  // waves that run them
     constexpr int PQ = (MT * 1024 + NT - 1) / NT < 4 ? (MT * 1024 + NT - 1) / NT : 4;
+    // 16-byte stream loads per lane and group: a wave's G rows hold at most 2 * CH * LPR
+    // blocks each, G * 2 * CH * LPR * 18 = 2304 * CH bytes.
+    constexpr int LS = (2304 / 16 * CH + kWave - 1) / kWave;
     static_assert(P2 <= kWaves, "phase 2 needs four lanes per row and row of x");
+    static_assert(!kStream || (MT == 1 && CH <= 2), "streamed groups: one row of x, at most two pairs a lane");
+    static_assert(!kNorm || (MT == 1 && CH <= 2), "the fused norm: one row of x, K <= 8192");
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ int bad[MT];
     __shared__ float wave_sum[NT / kWave];
@@ -451,19 +466,81 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
     if (threadIdx.x < MT) bad[threadIdx.x] = 0;
     lds_barrier();
 
-    // Unconditional loads from a clamped row and pair, so the compiler's wait counts stay exact.
-    auto load_group = [&](int it, uint32_t (&w)[CH][D]) {
-        const int r = min(row0 + it * kRows + rl, row_end - 1);
-        const uint8_t* base = W + r * row_bytes;
+    // kStream: this wave's staging region, G rows (after the x quants, the phase-1 buffers and
+    // the fused norm's x).
+    const int stage_words = x_words + nbuf * buf_floats + (kNorm ? K + (8 << norm_depth) : 0);
+    uint8_t* const stage = reinterpret_cast<uint8_t*>(lds + stage_words) + static_cast<size_t>(wave) * G * row_bytes;
+    const int stage_chunks = static_cast<int>(G * row_bytes / 16);
+
+    typedef uint32_t PairBuf[CH][D];
+    typedef u32x4 StreamBuf[LS];
+    typedef std::conditional_t<kStream != 0, StreamBuf, PairBuf> WBuf;
+    WBuf wa, wb;
+    float ya = 0.0f, yb = 0.0f;  // streamed groups: the outputs of the groups in wa, wb
+
+    // Phase 2 of group it runs on P2 waves, rotating with the group: chain c = 64 * (wave's
+    // turn) + lane is reference lane k = c & 3 of row r = (c >> 2) % kRows against row
+    // m = (c >> 2) / kRows of x; it adds the row's blocks in order, four per LDS read.
+    auto turn_of = [&](int it) {
+        const int t = wave - (it % kWaves) * P2 % kWaves;
+        return t < 0 ? t + kWaves : t;
+    };
+    auto chain_of = [&](int it) { return turn_of(it) * kWave + lane; };
+    // The output such a lane adds to (accumulate), read before the next group's weight loads
+    // are issued, from a clamped index on every lane: its wait never waits for those loads.
+    auto y_prior = [&](int it) {
+        const int c = chain_of(it);
+        const int m = min((c >> 2) / kRows, M - 1);
+        const int row = min(row0 + it * kRows + (c >> 2) % kRows, row_end - 1);
+        return y[static_cast<size_t>(m) * ldy + (silu_pairs ? row >> 1 : row)];
+    };
+
+    // Unconditional loads from a clamped row and pair (or chunk), so the compiler's wait
+    // counts stay exact.  A group past the last (the prefetch of the last groups) reads the
+    // first bytes of x instead, the same for every lane: one line that every workgroup has
+    // just read (cached), so these loads return quickly and move no weight bytes.
+    const uint8_t* const dummy = reinterpret_cast<const uint8_t*>(x);
+    auto load_group = [&](int it, WBuf& w) {
+        const bool live = it < iters;
+        if constexpr (kStream != 0) {
+            const size_t first = static_cast<size_t>(row0 + it * kRows + wave * G) * row_bytes;
+            const size_t last = static_cast<size_t>(row_end) * row_bytes - 16;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int p = min(j + c * LPR, pairs - 1);
-            load_pair<D>(base + static_cast<size_t>(p) * (2 * kQ4_0Bytes), w[c]);
+            for (int u = 0; u < LS; ++u) {
+                const int c = min(u * kWave + lane, stage_chunks - 1);
+                const uint8_t* a = live ? W + min(first + 16 * c, last) : dummy;
+                w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a4*>(a));
+            }
+        } else {
+            const int r = min(row0 + it * kRows + rl, row_end - 1);
+            const int p0 = min(j, pairs - 1);
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int p = min(p0 + c * LPR, pairs - 1);
+                load_pair<D>(live ? W + r * row_bytes + static_cast<size_t>(p) * (2 * kQ4_0Bytes) : dummy, w[c]);
+            }
+        }
+    };
+    // The first weight loads, group 0 (two groups ahead: with its output, which is read before
+    // its weights, so that waiting for the weights covers it).  Group 1 follows once x is
+    // quantized: issued together, the two groups delay x behind twice the traffic.
+    auto first_loads = [&]() {
+        if constexpr (kStream == 2) ya = y_prior(0);
+        load_group(0, wa);
+    };
+    // The pair (c) of this lane: from the registers, or (kStream) from the wave's staging region.
+    auto pair_of = [&](const WBuf& w, int c, int p, uint32_t (&out)[D]) {
+        if constexpr (kStream != 0) {
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(stage + g * row_bytes + static_cast<size_t>(p) * 36);
+#pragma unroll
+            for (int k = 0; k < D; ++k) out[k] = src[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < D; ++k) out[k] = w[c][k];
         }
     };
 
-    uint32_t wa[CH][D], wb[CH][D];
-    if (norm_w) {
+    if constexpr (kNorm) {
         // x and the norm weights first (at most 4 quads a thread: K <= 16 * NT), then the first
         // weights, so that waiting for x does not wait for W.
         float* xf = part0 + nbuf * buf_floats;  // K floats
@@ -485,7 +562,7 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
         // arrived with the weights (measured in the decode step: ~2900 cycles later).
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        load_group(0, wa);
+        first_loads();
         __builtin_amdgcn_sched_barrier(0);
         // x into LDS with 8 spare floats after every leaf of the pairwise tree (leaves of
         // K >> depth values: the host checks they are equal), read back conflict-free by the sum.
@@ -516,7 +593,7 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();  // every wave's x loads ahead of all weight loads, as above
         __builtin_amdgcn_sched_barrier(0);
-        load_group(0, wa);
+        first_loads();
         __builtin_amdgcn_sched_barrier(0);
         xp.template quantize<true, false, true>(x, ldx, M, K, lds_q, lds_cb, lds_dx, bad);
         lds_barrier();
@@ -550,23 +627,6 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
                 *reinterpret_cast<float2*>(scl + (m * kRows + rl) * S + 2 * p) = make_float2(hA * d2.x, hB * d2.y);
             }
         }
-    };
-
-    // Phase 2 of group it runs on P2 waves, rotating with the group: chain c = 64 * (wave's
-    // turn) + lane is reference lane k = c & 3 of row r = (c >> 2) % kRows against row
-    // m = (c >> 2) / kRows of x; it adds the row's blocks in order, four per LDS read.
-    auto turn_of = [&](int it) {
-        const int t = wave - (it % kWaves) * P2 % kWaves;
-        return t < 0 ? t + kWaves : t;
-    };
-    auto chain_of = [&](int it) { return turn_of(it) * kWave + lane; };
-    // The output such a lane adds to (accumulate), read before the next group's weight loads
-    // are issued, from a clamped index on every lane: its wait never waits for those loads.
-    auto y_prior = [&](int it) {
-        const int c = chain_of(it);
-        const int m = min((c >> 2) / kRows, M - 1);
-        const int row = min(row0 + it * kRows + (c >> 2) % kRows, row_end - 1);
-        return y[static_cast<size_t>(m) * ldy + (silu_pairs ? row >> 1 : row)];
     };
 
     auto phase2 = [&](int it, float y_old, const float* part, const float* scl) {
@@ -623,27 +683,64 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
     // One group: every wave's phase 1 into the group's buffer, a workgroup barrier, phase 2
     // on P2 waves.  With two buffers the next group's phase 1 overlaps this phase 2 (the
     // barrier after it orders the reuse of this buffer); with one, a second barrier does.
-    auto body = [&](int it, uint32_t (&cur)[CH][D], uint32_t (&nxt)[CH][D]) {
-        const float y_old = y_prior(it);
-        load_group(it + 1 < iters ? it + 1 : it, nxt);  // the last group reloads its own (cached) bytes
+    // cur holds group it (in flight or arrived), nxt group it + 1 (in flight).  Pair loads:
+    // group it + 1 is issued into nxt here.  Streamed groups: group it + 1 is already in flight
+    // in nxt; once cur is staged in LDS its registers take group it + 2, so two groups stay in
+    // flight through both phases.
+    auto body = [&](int it, WBuf& cur, WBuf& nxt, float& ycur) {
         float* part = part0 + (nbuf == 2 ? (it & 1) * buf_floats : 0);
         float* scl = part + 4 * M * kRows * S;
+        float y_old;
+        // This wave's rows into its staging region (its previous group's reads are done: LDS
+        // operations of a wave complete in order).
+        auto stage_cur = [&]() {
+            if constexpr (kStream != 0) {
+#pragma unroll
+                for (int u = 0; u < LS; ++u) {
+                    const int c = u * kWave + lane;
+                    if (c < stage_chunks) *reinterpret_cast<u32x4*>(stage + 16 * c) = cur[u];
+                }
+            }
+        };
+        if constexpr (kStream == 2) {
+            stage_cur();
+            y_old = ycur;
+            ycur = y_prior(it + 2);
+            load_group(it + 2, cur);
+            wave_lds_sync();
+        } else if constexpr (kStream == 1) {
+            y_old = y_prior(it);
+            load_group(it + 1, nxt);
+            stage_cur();
+            wave_lds_sync();
+        } else {
+            y_old = y_prior(it);
+            load_group(it + 1, nxt);
+        }
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int p = j + c * LPR;
-            if (p < pairs) phase1(p, cur[c], part, scl);
+            if (p < pairs) {
+                uint32_t w[D];
+                pair_of(cur, c, p, w);
+                phase1(p, w, part, scl);
+            }
         }
         lds_barrier();
         phase2(it, y_old, part, scl);
         if (nbuf == 1) lds_barrier();
     };
 
+    if constexpr (kStream == 2) {
+        yb = y_prior(1);
+        load_group(1, wb);
+    }
     int it = 0;
     for (; it + 1 < iters; it += 2) {
-        body(it, wa, wb);
-        body(it + 1, wb, wa);
+        body(it, wa, wb, ya);
+        body(it + 1, wb, wa, yb);
     }
-    if (it < iters) body(it, wa, wb);
+    if (it < iters) body(it, wa, wb, ya);
 }
 
 // Odd K/32 or a 2-byte aligned W: four lanes per row walk the blocks themselves (16-bit
@@ -901,7 +998,27 @@ struct NormArgs {
     double eps = 0.0;
     int depth = -1;
     int silu_pairs = 0;  // epilogue: rows (2n, 2n+1) -> y[n] = silu(row 2n) * row 2n+1
+    int stream = 0;      // GemvTuning::stream_weights
 };
+
+template <int LPR, int MT, int NT, int CH, int kStream, bool kNorm>
+hipError_t launch_ordered_kernel(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
+                                 int rows_per_wg, int acc, const NormArgs& nrm, int nbuf, size_t lds,
+                                 hipStream_t stream) {
+    const int grid = (N + rows_per_wg - 1) / rows_per_wg;
+    if (const hipError_t e = allow_lds(gemv_q4_ordered_kernel<LPR, MT, NT, CH, kStream, kNorm>, lds); e != hipSuccess)
+        return e;
+    hipLaunchKernelGGL((gemv_q4_ordered_kernel<LPR, MT, NT, CH, kStream, kNorm>), dim3(grid), dim3(NT), lds, stream, M, N,
+                       K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm.w, nrm.eps, nrm.depth, nrm.silu_pairs, nbuf);
+    return hipGetLastError();
+}
+
+// Streamed weight groups (kStream of gemv_q4_ordered_kernel): SMK_Q4_STREAM=0 pair loads,
+// 1 one group ahead, 2 two groups ahead (diagnostics); unset: the built-in choice (-1).
+const int g_q4_stream = [] {
+    const char* v = std::getenv("SMK_Q4_STREAM");
+    return v && v[0] >= '0' && v[0] <= '2' ? v[0] - '0' : -1;
+}();
 
 template <int LPR, int MT, int NT, int CH>
 hipError_t launch_ordered_ch(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
@@ -911,15 +1028,40 @@ hipError_t launch_ordered_ch(int M, int N, int K, const float* x, int ldx, const
     if (nrm.silu_pairs && (LPR > 32 || (rows_per_wg & 1) || accumulate_unsupported(acc))) return hipErrorInvalidValue;
     if (rows_per_wg <= 0) rows_per_wg = std::max(kRows, (N + 511) / 512);
     const size_t extra = nrm.w ? (static_cast<size_t>(K) + (8u << nrm.depth)) * 4 : 0;
+    const size_t nb = static_cast<size_t>(K) >> 5;
+    // Streamed groups: every row is whole 16-byte chunks (K % 256 == 0) and W is 16-byte
+    // aligned, so a chunk that holds any byte of a workgroup's rows lies inside them; the
+    // staging regions take kRows rows of LDS.
+    const bool stream_shape = MT == 1 && CH <= 2 && g_q4_stream != 0 && nb % 8 == 0 &&
+                              reinterpret_cast<uintptr_t>(W) % 16 == 0;
+    const size_t stage = stream_shape ? kRows * nb * kQ4_0Bytes : 0;
+    constexpr size_t kCap = 150 * 1024;
     // Two phase-1 buffers (phase 2 of a group overlaps the next group's phase 1) when a
     // workgroup has several groups and they fit.
-    const int nbuf = (rows_per_wg > kRows && ordered_lds_bytes(M, K, kRows, 2) + extra <= 150 * 1024) ? 2 : 1;
+    const int nbuf = (rows_per_wg > kRows && ordered_lds_bytes(M, K, kRows, 2) + extra + stage <= kCap) ? 2 : 1;
     const size_t lds = ordered_lds_bytes(M, K, kRows, nbuf) + extra;
-    const int grid = (N + rows_per_wg - 1) / rows_per_wg;
-    if (const hipError_t e = allow_lds(gemv_q4_ordered_kernel<LPR, MT, NT, CH>, lds); e != hipSuccess) return e;
-    hipLaunchKernelGGL((gemv_q4_ordered_kernel<LPR, MT, NT, CH>), dim3(grid), dim3(NT), lds, stream, M, N, K, x, ldx,
-                       W, y, ldy, rows_per_wg, acc, nrm.w, nrm.eps, nrm.depth, nrm.silu_pairs, nbuf);
-    return hipGetLastError();
+    if constexpr (MT == 1 && CH <= 2) {
+        const bool st = stream_shape && lds + stage <= kCap;
+        const size_t bytes = lds + (st ? stage : 0);
+        // Measured on MI355X (us, cached pair loads / one group ahead / two ahead): workgroups of
+        // many groups stream best two ahead (lm_head 128256x2048 34.1 / 34.6 / 31.9); with a few
+        // groups or one the cached pair loads are as fast or faster on their own (14336x4096
+        // 11.1 / 11.5 / 11.8, 8192x2048 4.31 / 4.46 / 4.46), but inside a decode step one group
+        // ahead is faster (1,557 / 1,616 tok/s with every GEMV in one mode): the non-temporal
+        // weights leave the activations and the KV cache in the caches.
+        const int groups = (rows_per_wg + kRows - 1) / kRows;
+        const int mode = !st ? 0 : g_q4_stream > 0 ? g_q4_stream : groups >= 8 ? 2 : nrm.stream ? 1 : 0;
+#define SMK_ORDERED(S, NORM) \
+    launch_ordered_kernel<LPR, MT, NT, CH, S, NORM>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, nbuf, bytes, stream)
+        if (nrm.w) return mode == 2 ? SMK_ORDERED(2, true) : mode == 1 ? SMK_ORDERED(1, true) : SMK_ORDERED(0, true);
+        if (mode == 2) return SMK_ORDERED(2, false);
+        if (mode == 1) return SMK_ORDERED(1, false);
+#undef SMK_ORDERED
+    } else {
+        if (nrm.w) return hipErrorInvalidValue;  // the fused norm covers K <= 8192: at most two pairs a lane
+    }
+    return launch_ordered_kernel<LPR, MT, NT, CH, 0, false>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, nbuf,
+                                                            lds, stream);
 }
 
 // Pairs per lane and row: 1, 2, 4 or 8 (the lane split is raised until that suffices).
@@ -964,6 +1106,7 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
     constexpr size_t kLdsCap = 150 * 1024;
     const bool generic = !pair_path_ok(K, W) || ordered_lds_bytes(M, K, 256 / 64) > kLdsCap || pairs > 8 * 64;
     NormArgs nrm;
+    nrm.stream = t ? t->stream_weights : 0;
     if (t && t->silu_pairs) {
         if (M != 1 || generic || (N & 1)) return hipErrorInvalidValue;
         nrm.silu_pairs = 1;

@@ -27,6 +27,9 @@ struct GemvTuning {
                                     // y[n] = silu(gate) * up (y has N / 2 entries)
     int mfma_min_rows = 0;          // Q4_0 in the reference order: rows of x from which the
                                     // matrix-core kernel takes the product (0: built-in choice)
+    int stream_weights = 0;         // Q4_0, one row of x: 1 streams the weights with
+                                    // non-temporal loads wherever the shape allows (a decode
+                                    // step: the caches keep its activations and KV cache)
 };
 
 // y[m*ldy + n] = sum_k x[m*ldx + k] * W[n][k] for m < M, W in GGUF Q4_0 (block_bytes 18) or
