@@ -407,7 +407,7 @@ def main() -> int:
         finally:
             dev.abi.call("smk_set_q4_order", 1)
         cases.update(batched_cases(dev, st, wu, args.mode))
-    roof = read_roof(dev)
+    roof = read_roof(dev, nontemporal=1)
     copy = copy_roof(dev)
     decode = decode_case() if args.cases == "all" else None
     sec = head["us"] * 1e-6
