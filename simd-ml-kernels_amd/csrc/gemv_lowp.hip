@@ -47,7 +47,9 @@ __device__ __forceinline__ void widen(const u32x4& t, float* v) {
 // LPR lanes share a row; a lane takes 8-element groups j, j + LPR, ... of its U rows.  The
 // loads of the next D groups are issued before the current D groups' FMAs (two register
 // buffers), every load unconditional from a clamped row and group so the compiler's wait
-// counts stay exact.  FP32 B takes two 16-byte loads per group.
+// counts stay exact.  FP32 B takes two 16-byte loads per group.  B is read with non-temporal
+// loads: the LPR lanes of a row read LPR * 16 contiguous bytes, whole lines that no later
+// load touches (measured on MI355X, f16 4096x14336 23.0 -> 20.6 us, 14336x4096 22.6 -> 21.1).
 template <int E, int LPR, int U, int MT, int D>
 __global__ __launch_bounds__(kThreads) void gemv_lowp_kernel(int M, int N, int K, float alpha,
                                                              const void* __restrict__ A, int lda,
@@ -85,7 +87,8 @@ __global__ __launch_bounds__(kThreads) void gemv_lowp_kernel(int M, int N, int K
                 for (int u = 0; u < U; ++u)
 #pragma unroll
                     for (int h = 0; h < L; ++h)
-                        w[d][u][h] = reinterpret_cast<const u32x4*>(rows[u] + (static_cast<size_t>(k0) + 8 * c) * kEs)[h];
+                        w[d][u][h] = __builtin_nontemporal_load(
+                            reinterpret_cast<const u32x4*>(rows[u] + (static_cast<size_t>(k0) + 8 * c) * kEs) + h);
             }
         };
         u32x4 wa[D][U][L], wb[D][U][L];
