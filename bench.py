@@ -389,8 +389,10 @@ def main() -> int:
         st, wu = max(200, args.steps // 4), 50
         cases["q8_0_8192x2048"] = quant_case(dev, "q8_0", 8192, 2048, 1, st, wu, args.mode)
         cases["q8_0_2048x8192"] = quant_case(dev, "q8_0", 2048, 8192, 1, st, wu, args.mode)
-        cases["q4_0_14336x4096"] = quant_case(dev, "q4_0", 14336, 4096, 3, st, wu, args.mode)
-        cases["q8_0_14336x4096"] = quant_case(dev, "q8_0", 14336, 4096, 3, st, wu, args.mode)
+        # The Llama-3-8B shapes of the north-star target (FFN up/gate, down, attention out).
+        for fmt in ("q4_0", "q8_0"):
+            for N, K in ((14336, 4096), (4096, 14336), (4096, 4096)):
+                cases[f"{fmt}_{N}x{K}"] = quant_case(dev, fmt, N, K, 3, st, wu, args.mode)
         for fmt in ("f16", "bf16"):
             for N, K in ((14336, 4096), (4096, 14336), (4096, 4096)):
                 cases[f"{fmt}_{N}x{K}"] = lowp_case(dev, fmt, N, K, 2, max(60, st // 8), 10, args.mode)
