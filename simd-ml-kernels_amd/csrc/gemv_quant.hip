@@ -1210,20 +1210,24 @@ hipError_t gemv_quant_fmt(int M, int N, int K, const float* x, int ldx, const ui
             default: return launch_generic<BB, 8>(M, N, K, x, ldx, W, y, ldy, acc, stream);
         }
     }
-    // The lane split fixes the summation order, so it depends on K only: every row of a
+    // The lane split fixes the summation order, so it depends on the shape only: every row of a
     // batched call then equals the single-row call bit for bit.  64 lanes per row once a row
-    // holds >= 128 pairs, else 32 (measured best on MI355X for the BASELINE shapes).
+    // holds >= 128 pairs, or >= 64 pairs with N <= 4096; else 32 (measured best on MI355X for the
+    // BASELINE and Llama-3-8B shapes: Q8_0 4096x4096 5.68 -> 5.20 us with 64).
     const int pairs = (K >> 5) / 2;
-    const int lpr = (t && t->lanes_per_row) ? t->lanes_per_row
-                                            : (pairs >= 128 ? 64 : (pairs >= 32 ? 32 : choose_lpr(pairs)));
+    const int lpr = (t && t->lanes_per_row)
+                        ? t->lanes_per_row
+                        : (pairs >= 128 || (pairs >= 64 && N <= 4096) ? 64 : (pairs >= 32 ? 32 : choose_lpr(pairs)));
     int rpw = t ? t->rows_per_wg : 0;
     if (mt == 1) {
         // One row of x (decode).  Measured on MI355X over the BASELINE shapes (9.4 MB to 295 MB
         // of weights): one pair per lane per step; 1024-thread workgroups for small and very
         // large matrices, 512 in between; 1, 2 or 4 workgroups per CU with the rows split evenly.
+        // Rows of K >= 8192: one workgroup per CU (Q8_0 4096x14336 15.1 -> 13.9 us).
         const double bytes = static_cast<double>(N) * (K >> 5) * BB;
-        const int nt_auto = (bytes < 24e6 || bytes >= 128e6) ? 1024 : 512;
-        const int per_cu = bytes < 24e6 ? 1 : (bytes < 128e6 ? 2 : 4);
+        const bool one = bytes < 24e6 || K >= 8192;
+        const int nt_auto = (one || bytes >= 128e6) ? 1024 : 512;
+        const int per_cu = one ? 1 : (bytes < 128e6 ? 2 : 4);
         if (rpw <= 0) rpw = std::max(1, (N + g_cus * per_cu - 1) / (g_cus * per_cu));
         // No more waves than rows: a wave covers 64 / lpr rows per step.
         int nt = (t && t->threads) ? t->threads : nt_auto;
