@@ -146,6 +146,32 @@ __device__ __forceinline__ uint32_t q8_quad(const float (&v)[4], float& d, int (
            ((static_cast<uint32_t>(q[2]) & 0xffu) << 16) | (static_cast<uint32_t>(q[3]) << 24);
 }
 
+// Q8 quants of two quads of x, k and k + 4 (values 4k..4k+3 and 16+4k..16+4k+3) of a
+// 32-value block whose four lanes (k = 0..3) call this together: the same arithmetic as q8_quad
+// (the block's amax is a max, exact in any order), its two IEEE divisions done once for eight
+// values.  fa / fb: the finite flags of the two quads (a quad with a NaN or an infinity keeps
+// q = 0); pa / pb: their quants as bytes of one dword each.
+__device__ __forceinline__ void q8_oct(const float (&va)[4], const float (&vb)[4], float& d, int (&qa)[4],
+                                       int (&qb)[4], int& fa, int& fb, uint32_t& pa, uint32_t& pb) {
+    fa = finite_bits(va[0]) & finite_bits(va[1]) & finite_bits(va[2]) & finite_bits(va[3]);
+    fb = finite_bits(vb[0]) & finite_bits(vb[1]) & finite_bits(vb[2]) & finite_bits(vb[3]);
+    float amax = fmaxf(fmaxf(fmaxf(fabsf(va[0]), fabsf(va[1])), fmaxf(fabsf(va[2]), fabsf(va[3]))),
+                       fmaxf(fmaxf(fabsf(vb[0]), fabsf(vb[1])), fmaxf(fabsf(vb[2]), fabsf(vb[3]))));
+    amax = group_max<4>(amax);
+    d = amax / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    if (!(id <= 3.40282347e38f)) id = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        qa[i] = fa ? round_half_away(va[i] * id) : 0;
+        qb[i] = fb ? round_half_away(vb[i] * id) : 0;
+    }
+    pa = (static_cast<uint32_t>(qa[0]) & 0xffu) | ((static_cast<uint32_t>(qa[1]) & 0xffu) << 8) |
+         ((static_cast<uint32_t>(qa[2]) & 0xffu) << 16) | (static_cast<uint32_t>(qa[3]) << 24);
+    pb = (static_cast<uint32_t>(qb[0]) & 0xffu) | ((static_cast<uint32_t>(qb[1]) & 0xffu) << 8) |
+         ((static_cast<uint32_t>(qb[2]) & 0xffu) << 16) | (static_cast<uint32_t>(qb[3]) << 24);
+}
+
 // The reference's vectorised exp (simd_math.hpp:63-117, used by its SiLU and softmax): clamp
 // to +-88.3762626647949 (a NaN becomes the bound, as vminps/vmaxps return their second
 // operand), k = floor(z*log2e + 0.5) with one fused multiply-add, Cody-Waite reduction

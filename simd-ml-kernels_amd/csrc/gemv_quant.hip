@@ -94,54 +94,92 @@ __device__ __forceinline__ void quantize_quad(const float (&v)[4], int m, int kq
     }
 }
 
+// Two quads of x, k and k + 4 of block b (four consecutive threads hold the block, k = 0..3),
+// into the LDS quants, biases and scale as quantize_quad stores them.  The reference lane k of
+// the Q4_0 order owns exactly these two quads, so its chain bias needs no other lane.
+template <bool kPlanes, bool kBias, bool kChainBias = false>
+__device__ __forceinline__ void quantize_oct(const float (&va)[4], const float (&vb)[4], int m, int b, int k, int K,
+                                             uint32_t* lds_q, int* lds_bias, float* lds_dx, int* bad,
+                                             bool live = true) {
+    const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
+    float d;
+    int qa[4], qb[4], fa, fb;
+    uint32_t pa, pb;
+    q8_oct(va, vb, d, qa, qb, fa, fb, pa, pb);
+    const int s8 = qa[0] + qa[1] + qa[2] + qa[3] + qb[0] + qb[1] + qb[2] + qb[3];
+    const int s = kBias ? group_sum_int<4>(s8) : 0;
+    if (live) {
+        lds_q[m * quads + x_dword_index<kPlanes>(b, k, pairs)] = pa;
+        lds_q[m * quads + x_dword_index<kPlanes>(b, k + 4, pairs)] = pb;
+        if (kChainBias) lds_bias[(m * nb + b) * 4 + k] = -8 * s8;
+        if (kBias && k == 0) lds_bias[m * nb + b] = -8 * s;
+        if (k == 0) lds_dx[m * nb + b] = d;
+        if (!(fa & fb)) bad[m] = 1;
+    }
+}
+
 // The first PQ quads a thread quantizes are loaded into registers before the kernel issues
 // its weight loads, so that waiting for x does not wait for W (global loads retire in
 // order); quads past PQ * NT (very long rows) are loaded and quantized afterwards.
 template <int NT, int PQ, int MT>
 struct XPreload {
-    float v[PQ][4];
-    // A wave loads pass p only when one of its lanes has a quad there (waves past the end of
+    // Units of eight values ("octs", two quads k and k + 4 of one block, quantize_oct): oct o of
+    // row m is block o / 4, k = o % 4.  PQ octs a thread are loaded before the weights.
+    float va[PQ][4], vb[PQ][4];
+    // A wave loads pass p only when one of its lanes has an oct there (waves past the end of
     // x neither load nor quantize, and leave the SIMD to those that do).  Within a loading
-    // wave the loads are unconditional (an index past the end reloads quad 0), so the wait
+    // wave the loads are unconditional (an index past the end reloads oct 0), so the wait
     // for x has a known count of younger loads and does not wait for the weights issued
     // after it.  The loads sit in blocks of their own, ahead of the weight loads: a load in
-    // the same block as a wave-uniform branch to its only use is moved into that branch by
-    // the compiler, behind the weights.
+    // the same block as a wave-uniform branch to its only use is moved by the compiler into
+    // that branch, behind the weights.
     __device__ __forceinline__ static bool wave_has(int p, int total) {
         return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) & ~(kWave - 1)) + p * NT < total;
     }
+    __device__ __forceinline__ static const float* oct_src(const float* x, int ldx, int octs, int o) {
+        const int m = MT == 1 ? 0 : o / octs, r = o - m * octs;
+        return x + static_cast<size_t>(m) * ldx + 32 * (r >> 2) + 4 * (r & 3);
+    }
     __device__ __forceinline__ void load(const float* __restrict__ x, int ldx, int M, int K) {
-        const int quads = K >> 2, total = M * quads;
+        const int octs = K >> 3, total = M * octs;
 #pragma unroll
         for (int p = 0; p < PQ; ++p) {
             if (!wave_has(p, total)) break;
-            int qd = static_cast<int>(threadIdx.x) + p * NT;
-            qd = qd < total ? qd : 0;
-            const int m = MT == 1 ? 0 : qd / quads, kq = qd - m * quads;
-            const f32x4a4 t = *reinterpret_cast<const f32x4a4*>(x + static_cast<size_t>(m) * ldx + 4 * kq);
-            v[p][0] = t.x;
-            v[p][1] = t.y;
-            v[p][2] = t.z;
-            v[p][3] = t.w;
+            int o = static_cast<int>(threadIdx.x) + p * NT;
+            o = o < total ? o : 0;
+            const float* src = oct_src(x, ldx, octs, o);
+            const f32x4a4 a = *reinterpret_cast<const f32x4a4*>(src);
+            const f32x4a4 b = *reinterpret_cast<const f32x4a4*>(src + 16);
+            va[p][0] = a.x;
+            va[p][1] = a.y;
+            va[p][2] = a.z;
+            va[p][3] = a.w;
+            vb[p][0] = b.x;
+            vb[p][1] = b.y;
+            vb[p][2] = b.z;
+            vb[p][3] = b.w;
         }
     }
     template <bool kPlanes, bool kBias, bool kChainBias = false>
     __device__ __forceinline__ void quantize(const float* __restrict__ x, int ldx, int M, int K, uint32_t* lds_q,
                                              int* lds_bias, float* lds_dx, int* bad) {
-        const int quads = K >> 2, total = M * quads;
+        const int octs = K >> 3, total = M * octs;
 #pragma unroll
         for (int p = 0; p < PQ; ++p) {
             if (!wave_has(p, total)) break;
-            const int qd = static_cast<int>(threadIdx.x) + p * NT;
-            const bool live = qd < total;
-            const int qe = live ? qd : 0, m = MT == 1 ? 0 : qe / quads;
-            quantize_quad<kPlanes, kBias, kChainBias>(v[p], m, qe - m * quads, K, lds_q, lds_bias, lds_dx, bad, live);
+            const int o = static_cast<int>(threadIdx.x) + p * NT;
+            const bool live = o < total;
+            const int oe = live ? o : 0, m = MT == 1 ? 0 : oe / octs, r = oe - m * octs;
+            quantize_oct<kPlanes, kBias, kChainBias>(va[p], vb[p], m, r >> 2, r & 3, K, lds_q, lds_bias, lds_dx, bad,
+                                                     live);
         }
-        for (int qd = static_cast<int>(threadIdx.x) + PQ * NT; qd < total; qd += NT) {
-            const int m = MT == 1 ? 0 : qd / quads, kq = qd - m * quads;
-            const f32x4a4 t = *reinterpret_cast<const f32x4a4*>(x + static_cast<size_t>(m) * ldx + 4 * kq);
-            const float u[4] = {t.x, t.y, t.z, t.w};
-            quantize_quad<kPlanes, kBias, kChainBias>(u, m, kq, K, lds_q, lds_bias, lds_dx, bad);
+        for (int o = static_cast<int>(threadIdx.x) + PQ * NT; o < total; o += NT) {
+            const int m = MT == 1 ? 0 : o / octs, r = o - m * octs;
+            const float* src = oct_src(x, ldx, octs, o);
+            const f32x4a4 a = *reinterpret_cast<const f32x4a4*>(src);
+            const f32x4a4 b = *reinterpret_cast<const f32x4a4*>(src + 16);
+            const float ua[4] = {a.x, a.y, a.z, a.w}, ub[4] = {b.x, b.y, b.z, b.w};
+            quantize_oct<kPlanes, kBias, kChainBias>(ua, ub, m, r >> 2, r & 3, K, lds_q, lds_bias, lds_dx, bad);
         }
     }
 };
@@ -262,11 +300,11 @@ __global__ __launch_bounds__(NT) void gemv_pairs_kernel(int M, int N, int K, con
     constexpr int G = kWave / LPR;                 // rows side by side in one wave
     constexpr int kWaves = NT / kWave;
     constexpr int kRowsPerIter = kWaves * G * U;   // rows one workgroup step covers
-    // Quads of x a thread loads before the weights: all of a row up to K = 4 * 8 * NT for one row
-    // of x (quads past them load and quantize one at a time, after the weights are in flight;
-    // sized for K <= 4096 this took Q8_0 4096x14336 from 14.6 to 16.4 us).
-    constexpr int PQ = MT == 1 ? (NT >= 1024 ? 4 : 8)
-                               : ((MT * 1024 + NT - 1) / NT < 4 ? (MT * 1024 + NT - 1) / NT : 4);
+    // Octs (eight values) of x a thread loads before the weights: all of a row up to K = 8 * 4 * NT
+    // for one row of x (octs past them load and quantize one at a time, after the weights are in
+    // flight; sized for K <= 4096 this took Q8_0 4096x14336 from 14.6 to 16.4 us).
+    constexpr int PQ = MT == 1 ? (NT >= 1024 ? 2 : 4)
+                               : ((MT * 512 + NT - 1) / NT < 2 ? (MT * 512 + NT - 1) / NT : 2);  // octs
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ int bad[MT];
 
@@ -437,9 +475,9 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
     constexpr int kRows = kWaves * G;        // rows of one group
     constexpr int kChains = 4 * kRows * MT;  // reference lanes of a group (phase 2), at most
     constexpr int P2 = (kChains + kWave - 1) / kWave;  // waves that run them
-    // Quads of x a thread loads before the weights: a row holds at most 16 * CH * LPR quads.
-    constexpr int PQN = (16 * CH * LPR * MT + NT - 1) / NT;
-    constexpr int PQ = PQN < 1 ? 1 : (PQN > 8 ? 8 : PQN);
+    // Octs of x a thread loads before the weights: a row holds at most 8 * CH * LPR octs.
+    constexpr int PQN = (8 * CH * LPR * MT + NT - 1) / NT;
+    constexpr int PQ = PQN < 1 ? 1 : (PQN > 4 ? 4 : PQN);
     // 16-byte stream loads per lane and group: a wave's G rows hold at most 2 * CH * LPR
     // blocks each, G * 2 * CH * LPR * 18 = 2304 * CH bytes.
     constexpr int LS = (2304 / 16 * CH + kWave - 1) / kWave;
