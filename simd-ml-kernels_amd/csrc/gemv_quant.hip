@@ -585,25 +585,19 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
     };
 
     if constexpr (kNorm) {
-        // x and the norm weights first (at most 2 octs, 16 values, a thread: K <= 16 * NT), then
-        // the first weights, so that waiting for x does not wait for W.  Oct o holds quads k and
-        // k + 4 of block o / 4, k = o % 4, as quantize_oct takes them.
+        // x and the norm weights first (at most 4 quads a thread: K <= 16 * NT), then the first
+        // weights, so that waiting for x does not wait for W.
         float* xf = part0 + nbuf * buf_floats;  // K floats
         const float4* x4 = reinterpret_cast<const float4*>(x);
         const float4* w4 = reinterpret_cast<const float4*>(norm_w);
-        const int octs = K >> 3;
-        auto quad_of = [](int o, int half) { return 8 * (o >> 2) + (o & 3) + 4 * half; };
-        float4 xr[2][2], wr[2][2];
+        float4 xr[4], wr[4];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            if (u * NT >= octs) break;  // uniform: no thread has an oct this far (no idle loads)
-            const int o = static_cast<int>(threadIdx.x) + u * NT;
-            const int c = o < octs ? o : 0;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                xr[u][h] = x4[quad_of(c, h)];
-                wr[u][h] = w4[quad_of(c, h)];
-            }
+        for (int u = 0; u < 4; ++u) {
+            if (u * NT >= quads) break;  // uniform: no thread has a quad this far (no idle loads)
+            const int qd = static_cast<int>(threadIdx.x) + u * NT;
+            const int c = qd < quads ? qd : 0;
+            xr[u] = x4[c];
+            wr[u] = w4[c];
         }
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_sched_barrier(0);
@@ -618,31 +612,22 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
         // K >> depth values: the host checks they are equal), read back conflict-free by the sum.
         const int leaf = K >> norm_depth;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int o = static_cast<int>(threadIdx.x) + u * NT;
-            if (o < octs)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int qd = quad_of(o, h);
-                    reinterpret_cast<float4*>(xf + 8 * ((4 * qd) / leaf))[qd] = xr[u][h];
-                }
+        for (int u = 0; u < 4; ++u) {
+            const int qd = static_cast<int>(threadIdx.x) + u * NT;
+            if (qd < quads) reinterpret_cast<float4*>(xf + 8 * ((4 * qd) / leaf))[qd] = xr[u];
         }
         lds_barrier();
         const float total = uniform_chunk_sum<NT>(xf, K, norm_depth, wave_sum, 8);
         const float var = static_cast<float>(static_cast<double>(total) / static_cast<double>(K));
         const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(var) + norm_eps));
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            if (u * NT >= octs) break;  // uniform: no thread has an oct this far
-            const int o = static_cast<int>(threadIdx.x) + u * NT;
-            const bool live = o < octs;
-            const int oe = live ? o : 0;
-            const float4 xa = xr[u][0], xb = xr[u][1], wa4 = wr[u][0], wb4 = wr[u][1];
-            const float ha[4] = {wa4.x * (xa.x * scale), wa4.y * (xa.y * scale), wa4.z * (xa.z * scale),
-                                 wa4.w * (xa.w * scale)};
-            const float hb[4] = {wb4.x * (xb.x * scale), wb4.y * (xb.y * scale), wb4.z * (xb.z * scale),
-                                 wb4.w * (xb.w * scale)};
-            quantize_oct<true, false, true>(ha, hb, 0, oe >> 2, oe & 3, K, lds_q, lds_cb, lds_dx, bad, live);
+        for (int u = 0; u < 4; ++u) {
+            if (u * NT >= quads) break;  // uniform: no thread has a quad this far
+            const int qd = static_cast<int>(threadIdx.x) + u * NT;
+            const bool live = qd < quads;
+            const float h[4] = {wr[u].x * (xr[u].x * scale), wr[u].y * (xr[u].y * scale),
+                                wr[u].z * (xr[u].z * scale), wr[u].w * (xr[u].w * scale)};
+            quantize_quad<true, false, true>(h, 0, live ? qd : 0, K, lds_q, lds_cb, lds_dx, bad, live);
         }
         lds_barrier();
     } else {
