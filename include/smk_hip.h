@@ -206,6 +206,13 @@ int smk_set_gemv_tuning(int lanes_per_row, int rows_per_wg, int threads, int unr
  * y bit-exact with its AVX2 / AVX-512 tables); 0 selects the free-order kernel, whose y is
  * within the reference's error bound, for speed comparisons. */
 int smk_set_q4_order(int reference_order);
+/* Diagnostics: how the reference-order Q4_0 kernel loads one row of x's weights: -1 (default)
+ * the built-in choice, 0 each lane its own 36-byte pairs (cached), 1 each wave its rows'
+ * contiguous bytes with non-temporal loads staged in LDS, one group of rows ahead, 2 the same two
+ * groups ahead (forms 1 and 2 apply where K % 256 == 0, W is 16-byte aligned and a lane takes at
+ * most two pairs a row).  y is the same bits in every form.  No reference counterpart: the
+ * reference reads its weights from host memory (q4_0_rows.hpp:71-167). */
+int smk_set_q4_stream(int mode);
 /* Diagnostics: rows of X from which a Q4_0 product (smk_gemm_q4_0, smk_d_gemm_q4_0) takes the
  * matrix-core kernel (0 = built-in choice; a large value keeps the launches of 8 GEMV rows).
  * No reference counterpart: the reference has no batched Q4_0 product (pybind_entry.cpp:956-957). */

@@ -1058,8 +1058,9 @@ hipError_t launch_ordered_kernel(int M, int N, int K, const float* x, int ldx, c
 }
 
 // Streamed weight groups (kStream of gemv_q4_ordered_kernel): SMK_Q4_STREAM=0 pair loads,
-// 1 one group ahead, 2 two groups ahead (diagnostics); unset: the built-in choice (-1).
-const int g_q4_stream = [] {
+// 1 one group ahead, 2 two groups ahead (diagnostics, also set_q4_stream); unset: the built-in
+// choice (-1).
+int g_q4_stream = [] {
     const char* v = std::getenv("SMK_Q4_STREAM");
     return v && v[0] >= '0' && v[0] <= '2' ? v[0] - '0' : -1;
 }();
@@ -1339,6 +1340,8 @@ hipError_t gemv_quant(int block_bytes, int M, int N, int K, const float* x, int 
 const char* gemv_quant_path(int, int, int K, const uint8_t* W) { return pair_path_ok(K, W) ? "pairs" : "generic"; }
 
 void set_compute_units(int cus) { g_cus = cus > 0 ? cus : 256; }
+
+void set_q4_stream(int mode) { g_q4_stream = mode; }
 
 hipError_t quantize_x_q8(int K, const float* x, int8_t* qs, float* dx, int* bad, hipStream_t stream) {
     if (K <= 0) return hipSuccess;

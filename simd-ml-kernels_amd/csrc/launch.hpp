@@ -57,6 +57,11 @@ hipError_t stream_workspace(hipStream_t stream, size_t bytes, void** out);
 // Compute units of the device (workgroup counts of the GEMV follow it).
 void set_compute_units(int cus);
 
+// Diagnostics: the weight-load form of the reference-order Q4_0 kernel for one row of x (-1 the
+// built-in choice, 0 pair loads, 1 streamed one group ahead, 2 two groups ahead; a form applies
+// where the shape allows it).  Not synchronised with launches in flight.
+void set_q4_stream(int mode);
+
 // Diagnostics: lanes per row (16, 32 or 64; 0 automatic) and rows per lane group (2 or 4) of
 // the FP16 / BF16 / FP32 GEMV.
 void set_lowp_tuning(int lanes_per_row, int unroll);

@@ -706,6 +706,12 @@ int smk_set_q4_order(int reference_order) {
     return ok();
 }
 
+int smk_set_q4_stream(int mode) {
+    if (mode < -1 || mode > 2) return fail(SMK_ERR_ARGUMENT, "mode must be -1, 0, 1 or 2");
+    smk::set_q4_stream(mode);
+    return ok();
+}
+
 int smk_set_q4_mfma_min_rows(int rows) {
     if (rows < 0) return fail(SMK_ERR_ARGUMENT, "rows must be >= 0");
     g_tuning.mfma_min_rows = rows;

@@ -208,6 +208,21 @@ class TestQ4ReferenceOrder:
             y = d_gemv("q4_0", x, wq, N, K, offset=off)
             np.testing.assert_array_equal(y.view(np.uint32), ref.view(np.uint32))
 
+    @pytest.mark.parametrize("mode", [0, 1, 2])
+    def test_every_weight_load_form_same_bits(self, mode):
+        """Pair loads, and weights streamed through LDS one or two groups of rows ahead
+        (smk_set_q4_stream): y bit-exact with the reference order in each form, at the decode
+        shapes, config 1, a Llama-3-8B shape and uneven workgroups."""
+        g.call("smk_set_q4_stream", mode)
+        try:
+            for N, K in ((8192, 2048), (3072, 2048), (16384, 2048), (2048, 8192), (1000, 4096), (14336, 4096)):
+                x, wq = _inputs("q4_0", N, K, 7 * N + K + mode)
+                y = d_gemv("q4_0", x, wq, N, K)
+                np.testing.assert_array_equal(y.view(np.uint32), o.gemv_q4_0_simd(x, wq, N, K).view(np.uint32),
+                                              err_msg=f"mode {mode} N={N} K={K}")
+        finally:
+            g.call("smk_set_q4_stream", -1)
+
     @pytest.mark.parametrize("lpr", [8, 16, 32, 64])
     def test_lane_split_does_not_change_bits(self, lpr):
         N, K = 131, 4096
