@@ -683,6 +683,23 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
             float a = 0.0f;
             const int n4 = nb >> 2;
             int q = 0;
+            // Batches of 32 blocks: all 16 reads of a batch are issued before its first FMA, so
+            // the chain waits for LDS once per 32 FMAs.
+            for (; q + 7 < n4; q += 8) {
+                float4 vv[8], ss[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    vv[i] = pv[q + i];
+                    ss[i] = sv[q + i];
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    a = fmaf(vv[i].x, ss[i].x, a);
+                    a = fmaf(vv[i].y, ss[i].y, a);
+                    a = fmaf(vv[i].z, ss[i].z, a);
+                    a = fmaf(vv[i].w, ss[i].w, a);
+                }
+            }
             for (; q + 1 < n4; q += 2) {
                 const float4 v0 = pv[q], v1 = pv[q + 1];
                 const float4 s0 = sv[q], s1 = sv[q + 1];
