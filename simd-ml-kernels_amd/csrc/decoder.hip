@@ -104,10 +104,15 @@ constexpr int kAttnThreads = 256;
 constexpr int kMaxTile = 256;
 constexpr size_t kAttnLdsBudget = 150 * 1024;
 
-// count floats (a multiple of 4, 16-byte aligned ends) from global to LDS: every thread issues
-// its 16-byte loads of a round before storing any (no load waits for an earlier store).
+// count floats (a multiple of 4, 16-byte aligned ends) from global to LDS, four rounds of
+// 256 x 16 bytes (of each source) a batch: every thread issues the batch's loads before storing
+// any. Every store is unconditional (an element past the end goes to the spare slot `dump`): a
+// load whose only use is a store under a branch is moved by the compiler into that branch, and
+// the rounds then wait for each other one at a time.
+template <bool kTwo>  // true: d1 from s1 as well
 __device__ __forceinline__ void stage_tiles(float* __restrict__ d0, const float* __restrict__ s0,
-                                            float* __restrict__ d1, const float* __restrict__ s1, int count) {
+                                            float* __restrict__ d1, const float* __restrict__ s1, int count,
+                                            float* __restrict__ dump) {
     const float4* a4 = reinterpret_cast<const float4*>(s0);
     const float4* b4 = reinterpret_cast<const float4*>(s1);
     const int n4 = count >> 2;
@@ -117,15 +122,13 @@ __device__ __forceinline__ void stage_tiles(float* __restrict__ d0, const float*
         for (int u = 0; u < 4; ++u) {
             const int e = base + u * kAttnThreads + static_cast<int>(threadIdx.x);
             va[u] = a4[e < n4 ? e : 0];
-            if (d1) vb[u] = b4[e < n4 ? e : 0];
+            if constexpr (kTwo) vb[u] = b4[e < n4 ? e : 0];
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int e = base + u * kAttnThreads + static_cast<int>(threadIdx.x);
-            if (e < n4) {
-                reinterpret_cast<float4*>(d0)[e] = va[u];
-                if (d1) reinterpret_cast<float4*>(d1)[e] = vb[u];
-            }
+            *reinterpret_cast<float4*>(e < n4 ? d0 + 4 * e : dump) = va[u];
+            if constexpr (kTwo) *reinterpret_cast<float4*>(e < n4 ? d1 + 4 * e : dump) = vb[u];
         }
     }
 }
@@ -174,47 +177,24 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     constexpr int kWaves = kAttnThreads / kWave;
     float* ktile = sc + ((cap + 3) & ~3);   // tile * hd
     float* vtile = ktile + tile * hd;       // tile * hd
+    float* dump = vtile + tile * hd;        // 4 floats: where stores past a tile's end go
     float* K = kc + static_cast<size_t>(g) * cap * hd;
     float* V = vc + static_cast<size_t>(g) * cap * hd;
     // This step's q, k, v and the first round's cached K and V (positions < pos), all loads
     // issued before any store.
     const int first_cached = min(min(tile, T), pos);
     {
-        const int d = threadIdx.x;
-        float q0 = 0.0f, k0 = 0.0f, v0 = 0.0f;
-        if (d < hd) {
-            q0 = qkv[static_cast<size_t>(head) * hd + d];
-            k0 = qkv[static_cast<size_t>(n_heads + g) * hd + d];
-            v0 = qkv[static_cast<size_t>(n_heads + n_kv + g) * hd + d];
-        }
-        const int n4 = first_cached * hd / 4;
-        constexpr int kPer = 16;  // float4 per thread: 256 positions of head_dim 64 (larger: the loop below)
-        float4 ka[kPer], va[kPer];
-        const float4* k4 = reinterpret_cast<const float4*>(K);
-        const float4* v4 = reinterpret_cast<const float4*>(V);
-#pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            const int e = u * kAttnThreads + static_cast<int>(threadIdx.x);
-            ka[u] = k4[e < n4 ? e : 0];
-            va[u] = v4[e < n4 ? e : 0];
-        }
-        if (d < hd) {
-            qs[d] = q0;
-            ks[d] = k0;
-            vs[d] = v0;
-        }
-#pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            const int e = u * kAttnThreads + static_cast<int>(threadIdx.x);
-            if (e < n4) {
-                reinterpret_cast<float4*>(ktile)[e] = ka[u];
-                reinterpret_cast<float4*>(vtile)[e] = va[u];
-            }
-        }
-        for (int e = kPer * kAttnThreads + static_cast<int>(threadIdx.x); e < n4; e += kAttnThreads) {
-            reinterpret_cast<float4*>(ktile)[e] = k4[e];  // head_dim > 64
-            reinterpret_cast<float4*>(vtile)[e] = v4[e];
-        }
+        // q, k, v loaded by every thread (a clamped index past head_dim; qs, ks, vs hold
+        // kAttnThreads entries, of which the first hd are read) and stored after the tiles, so
+        // their loads are not waited for before the tile loads are issued.
+        const int d = min(static_cast<int>(threadIdx.x), hd - 1);
+        const float q0 = qkv[static_cast<size_t>(head) * hd + d];
+        const float k0 = qkv[static_cast<size_t>(n_heads + g) * hd + d];
+        const float v0 = qkv[static_cast<size_t>(n_heads + n_kv + g) * hd + d];
+        stage_tiles<true>(ktile, K, vtile, V, first_cached * hd, dump);
+        qs[threadIdx.x] = q0;
+        ks[threadIdx.x] = k0;
+        vs[threadIdx.x] = v0;
     }
     __syncthreads();
     const float* cs = cos_tab + static_cast<size_t>(pos) * hd;
@@ -233,7 +213,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
         const int tn = min(tile, T - t0);
         const int cached = min(tn, pos - t0);  // positions of this round read from the cache
         __syncthreads();  // the previous round's tiles are consumed
-        if (cached > 0 && t0 > 0) stage_tiles(ktile, K + static_cast<size_t>(t0) * hd, nullptr, nullptr, cached * hd);
+        if (cached > 0 && t0 > 0) stage_tiles<false>(ktile, K + static_cast<size_t>(t0) * hd, nullptr, nullptr, cached * hd, dump);
         if (cached < tn)
             for (int d = threadIdx.x; d < hd; d += kAttnThreads) ktile[(pos - t0) * hd + d] = ks[d];
         __syncthreads();
@@ -314,7 +294,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
         const int tn = min(tile, T - t0);
         const int cached = min(tn, pos - t0);
         __syncthreads();  // probabilities written / the previous tile consumed
-        if (cached > 0 && t0 > 0) stage_tiles(vtile, V + static_cast<size_t>(t0) * hd, nullptr, nullptr, cached * hd);
+        if (cached > 0 && t0 > 0) stage_tiles<false>(vtile, V + static_cast<size_t>(t0) * hd, nullptr, nullptr, cached * hd, dump);
         if (cached < tn)
             for (int e = threadIdx.x; e < hd; e += kAttnThreads) vtile[(pos - t0) * hd + e] = vs[e];
         __syncthreads();
@@ -329,12 +309,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
 // Positions per round: the whole cache when it fits kMaxTile, else as many as the LDS budget
 // leaves beside the scores (at least 16).
 int attention_tile(int cap, int hd) {
-    const size_t left = kAttnLdsBudget / 4 - static_cast<size_t>((cap + 3) & ~3);
+    const size_t left = kAttnLdsBudget / 4 - static_cast<size_t>((cap + 3) & ~3) - 4;  // 4: the spare slot
     const int fit = static_cast<int>(left / (2 * static_cast<size_t>(hd)));
     return std::max(16, std::min({kMaxTile, cap, fit}));
 }
 size_t attention_lds(int cap, int hd) {
-    return (static_cast<size_t>((cap + 3) & ~3) + 2 * static_cast<size_t>(attention_tile(cap, hd)) * hd) * 4;
+    return (static_cast<size_t>((cap + 3) & ~3) + 2 * static_cast<size_t>(attention_tile(cap, hd)) * hd + 4) * 4;
 }
 
 // Prompt chunk: k = rope(k) and v of rows p < gridDim.y into the cache at pos_first + p, for KV
