@@ -213,6 +213,12 @@ int smk_set_q4_order(int reference_order);
  * most two pairs a row).  y is the same bits in every form.  No reference counterpart: the
  * reference reads its weights from host memory (q4_0_rows.hpp:71-167). */
 int smk_set_q4_stream(int mode);
+/* Diagnostics: the K-chunk tiled form of the reference-order Q4_0 GEMV for one row of x (tiles of
+ * 16 rows x 64 blocks streamed by 576 threads, a wave of its own for the FMA chains): 0 (default)
+ * the built-in choice, -1 never (the row-group kernel of smk_set_q4_stream instead), 2, 3 or 4
+ * that many tiles in flight wherever the shape allows it (K % 256 == 0, W 16-byte aligned).  y is
+ * the same bits either way.  No reference counterpart (its row loop is q4_0_rows.hpp:71-167). */
+int smk_set_q4_tiles(int tiles_in_flight);
 /* Diagnostics: rows of X from which a Q4_0 product (smk_gemm_q4_0, smk_d_gemm_q4_0) takes the
  * matrix-core kernel (0 = built-in choice; a large value keeps the launches of 8 GEMV rows).
  * No reference counterpart: the reference has no batched Q4_0 product (pybind_entry.cpp:956-957). */

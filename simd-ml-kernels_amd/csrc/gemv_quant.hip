@@ -804,6 +804,274 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
     if (it < iters) body(it, wa, wb, ya);
 }
 
+// ─── Q4_0 in the reference order over K-chunk tiles (one row of x) ──────────
+// The same arithmetic as gemv_q4_ordered_kernel, organised as a stream.  A workgroup (one per
+// compute unit) owns a contiguous range of rows and walks it in tiles of 16 rows x 64 blocks (a
+// 2048-value chunk of K): for each group of 16 rows, its K chunks in order.  A tile is
+// 16 x 1152 bytes = 1152 sixteen-byte pieces, each 16-byte aligned (K % 256 == 0); 576 threads
+// (9 waves) load exactly two pieces each with non-temporal loads, TF tiles ahead in registers.
+// (Measured on MI355X: aligned linear 16-byte loads stream 5.4 TB/s at 33 MB and 7.0 TB/s at
+// 295 MB; the 36-byte pairs loaded by their lanes -- two 4-byte-aligned 16-byte loads and a
+// dword -- only 4.1 and 5.7 TB/s.)  One workgroup barrier per tile:
+//   * every thread writes its two pieces of tile t into LDS stage buffer t % 2 and issues its
+//     loads of tile t + TF;
+//   * waves 0-7 ("dot waves"): lane (row 2w + lane / 32, pair lane % 32) reads its 36-byte pair
+//     from the stage buffer and writes the four reference lanes' exact integer dots of both
+//     blocks, as floats, and the two block scales fp16(d) * dx into dot buffer t % 2.  x's
+//     quants, chain biases and scales for the lane's pair position are held in registers when a
+//     row has at most two chunks (K <= 4096), else read from LDS once per tile;
+//   * wave 8 ("chain wave", issue priority raised): lane 4r + k runs reference lane k's FMA chain
+//     of row r over tile t - 1's blocks, in block order, carried in a register from chunk to
+//     chunk of the row group; after the group's last chunk, DPP adds (a0 + a2) + (a1 + a3) and
+//     lane k == 0 writes y.
+// Long rows advance all 64 chains of a row group together as their chunks arrive, and the FMA
+// chains run beside the next tile's dots on a wave of their own.
+namespace tiled {
+constexpr int kRows = 16;                                  // rows of a tile: 64 chains, one wave
+constexpr int kBlocks = 64;                                // blocks of a tile (2048 values of K)
+constexpr int kThreads = 576;                              // 8 dot waves + 1 chain wave
+constexpr int kChainWave = 8;
+constexpr int kRowBytes = kBlocks * kQ4_0Bytes;            // 1152: a row's share of a tile
+constexpr int kPiecesPerRow = kRowBytes / 16;              // 72
+constexpr int kPieces = kRows * kPiecesPerRow;             // 1152
+constexpr int kPiecesPerThread = kPieces / kThreads;       // 2
+constexpr int kStride = kBlocks + 4;                       // floats per dot row (4 mod 64: no conflicts)
+constexpr int kDotFloats = (4 * kRows + kRows) * kStride;  // [16][4][68] dots, then [16][68] scales
+static_assert(kPieces % kThreads == 0, "whole pieces per thread");
+static_assert((kThreads / kWave - 1) * kWave == kRows * kBlocks / 2, "one pair per dot lane");
+}  // namespace tiled
+
+__host__ __device__ __forceinline__ int tiled_x_words(int K) {
+    const int nb = K >> 5, quads = K >> 2;
+    return ((quads + nb + 3) & ~3) + nb * 4;
+}
+
+// x's Q8 data of one pair position: quants of both blocks (four planes), chain biases, scales.
+struct XPair {
+    uint4 q0, q1, q2, q3;
+    int4 bA, bB;
+    float2 d;
+};
+
+__device__ __forceinline__ XPair read_x_pair(const uint32_t* lds_q, const int* lds_cb, const float* lds_dx, int pairs,
+                                             int gp) {
+    const uint4* planes = reinterpret_cast<const uint4*>(lds_q);
+    XPair r;
+    r.q0 = planes[gp];
+    r.q1 = planes[pairs + gp];
+    r.q2 = planes[2 * pairs + gp];
+    r.q3 = planes[3 * pairs + gp];
+    r.bA = reinterpret_cast<const int4*>(lds_cb)[2 * gp];
+    r.bB = reinterpret_cast<const int4*>(lds_cb)[2 * gp + 1];
+    r.d = *reinterpret_cast<const float2*>(lds_dx + 2 * gp);
+    return r;
+}
+
+// TF: tiles in flight (register buffers); PQ: octs of x a thread loads before the weights;
+// XR: chunks per row whose x data the dot lanes hold in registers (1 or 2: the row has exactly
+// that many chunks; TF a multiple of XR), 0: read from LDS each tile.
+template <int TF, int PQ, int XR>
+__global__ __launch_bounds__(tiled::kThreads) void gemv_q4_tiled_kernel(int N, int K, const float* __restrict__ x,
+                                                                        const uint8_t* __restrict__ W,
+                                                                        float* __restrict__ y, int rows_per_wg,
+                                                                        int accumulate, int silu_pairs) {
+    constexpr int kThreads = tiled::kThreads, kRows = tiled::kRows, kBlocks = tiled::kBlocks;
+    constexpr int kRowBytes = tiled::kRowBytes, kPiecesPerRow = tiled::kPiecesPerRow, kPieces = tiled::kPieces;
+    constexpr int kPiecesPerThread = tiled::kPiecesPerThread, kStride = tiled::kStride;
+    constexpr int kDotFloats = tiled::kDotFloats, kChainWave = tiled::kChainWave;
+    static_assert(XR == 0 || TF % XR == 0, "the chunk of an unrolled step is static");
+    extern __shared__ __align__(16) uint32_t lds[];
+    __shared__ int bad[1];
+
+    const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
+    const size_t row_bytes = static_cast<size_t>(nb) * kQ4_0Bytes;
+    // LDS: x quants (four planes of pairs), dx [nb], chain biases [nb][4], two stage buffers of a
+    // tile's bytes, two dot buffers, and (accumulate) the prior y of the workgroup's rows.
+    uint32_t* lds_q = lds;
+    float* lds_dx = reinterpret_cast<float*>(lds + quads);
+    int* lds_cb = reinterpret_cast<int*>(lds + ((quads + nb + 3) & ~3));
+    const int x_words = tiled_x_words(K);
+    uint8_t* const stage0 = reinterpret_cast<uint8_t*>(lds + x_words);
+    float* const dots0 = reinterpret_cast<float*>(lds + x_words + 2 * kPieces * 4);
+    float* const y_prev = dots0 + 2 * kDotFloats;
+
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int row0 = blockIdx.x * rows_per_wg;
+    const int row_end = min(N, row0 + rows_per_wg);
+    const int chunks = (nb + kBlocks - 1) / kBlocks;
+    const int T = ((row_end - row0 + kRows - 1) / kRows) * chunks;
+
+    if (tid == 0) bad[0] = 0;
+    if (accumulate)
+        for (int i = tid; i < row_end - row0; i += kThreads) y_prev[i] = y[row0 + i];
+    lds_barrier();
+
+    // This thread's pieces: piece i = tid + u * kThreads of a tile is row i / 72, 16-byte unit
+    // i % 72 of that row's chunk (a partial last chunk clamps the unit; rows past the end clamp
+    // the row; both reload bytes some other piece loads).  Tiles past the last read the first
+    // 16 bytes of x instead (one line every lane shares): the load count stays fixed, so the
+    // compiler's waits stay exact, and no weight byte moves twice.
+    int pr[kPiecesPerThread], pq[kPiecesPerThread];
+#pragma unroll
+    for (int u = 0; u < kPiecesPerThread; ++u) {
+        const int i = tid + u * kThreads;
+        pr[u] = i / kPiecesPerRow;
+        pq[u] = i - pr[u] * kPiecesPerRow;
+    }
+    typedef u32x4 Slot[kPiecesPerThread];
+    auto load_tile = [&](int t, Slot& s) {
+        const bool live = t < T;
+        const int tt = live ? t : 0;
+        const int g = tt / chunks, c = tt - g * chunks;
+        const int units = min(kBlocks, nb - c * kBlocks) * kQ4_0Bytes / 16;
+#pragma unroll
+        for (int u = 0; u < kPiecesPerThread; ++u) {
+            const int row = min(row0 + g * kRows + pr[u], row_end - 1);
+            const uint8_t* src = W + static_cast<size_t>(row) * row_bytes + static_cast<size_t>(c) * kRowBytes +
+                                 16 * min(pq[u], units - 1);
+            if (!live) src = reinterpret_cast<const uint8_t*>(x);
+            s[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a4*>(src));
+        }
+    };
+    auto stage_tile = [&](int t, const Slot& s) {
+        uint8_t* st = stage0 + (t & 1) * (kPieces * 16);
+#pragma unroll
+        for (int u = 0; u < kPiecesPerThread; ++u)
+            *reinterpret_cast<u32x4*>(st + pr[u] * kRowBytes + 16 * pq[u]) = s[u];
+    };
+
+    // Phase 1 (dot waves) of tile t: the pair of this lane against x's data xp.
+    const int r1 = 2 * wave + (lane >> 5), p1 = lane & 31;
+    auto phase1 = [&](int t, const XPair& xp) {
+        const int g = t / chunks, c = t - g * chunks;
+        if (2 * p1 >= min(kBlocks, nb - c * kBlocks)) return;
+        const uint32_t* src =
+            reinterpret_cast<const uint32_t*>(stage0 + (t & 1) * (kPieces * 16) + r1 * kRowBytes + 36 * p1);
+        uint32_t w[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) w[k] = src[k];
+        uint32_t qa[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) qa[k] = skip2(w[k + 1], w[k]);
+        const float hA = half_bits_to_float(w[0]), hB = half_bits_to_float(w[4] >> 16);
+        float* dots = dots0 + (t & 1) * kDotFloats;
+        float* pr_ = dots + (4 * r1) * kStride + 2 * p1;
+        auto dots2 = [&](uint32_t qa_, uint32_t xa, uint32_t xb, int ba, uint32_t qb_, uint32_t xc, uint32_t xd, int bb) {
+            return make_float2(static_cast<float>(lane_dot(qa_, xa, xb, ba)),
+                               static_cast<float>(lane_dot(qb_, xc, xd, bb)));
+        };
+        *reinterpret_cast<float2*>(pr_) = dots2(qa[0], xp.q0.x, xp.q1.x, xp.bA.x, w[5], xp.q2.x, xp.q3.x, xp.bB.x);
+        *reinterpret_cast<float2*>(pr_ + kStride) = dots2(qa[1], xp.q0.y, xp.q1.y, xp.bA.y, w[6], xp.q2.y, xp.q3.y, xp.bB.y);
+        *reinterpret_cast<float2*>(pr_ + 2 * kStride) =
+            dots2(qa[2], xp.q0.z, xp.q1.z, xp.bA.z, w[7], xp.q2.z, xp.q3.z, xp.bB.z);
+        *reinterpret_cast<float2*>(pr_ + 3 * kStride) =
+            dots2(qa[3], xp.q0.w, xp.q1.w, xp.bA.w, w[8], xp.q2.w, xp.q3.w, xp.bB.w);
+        *reinterpret_cast<float2*>(dots + (4 * kRows + r1) * kStride + 2 * p1) = make_float2(hA * xp.d.x, hB * xp.d.y);
+    };
+
+    // Phase 2 (chain wave) of tile t: the chains of its row group over its blocks.
+    float acc = 0.0f;
+    auto phase2 = [&](int t) {
+        const int g = t / chunks, c = t - g * chunks;
+        const int cn = min(kBlocks, nb - c * kBlocks);  // a multiple of 8
+        const int r = lane >> 2, k = lane & 3;
+        const float* dots = dots0 + (t & 1) * kDotFloats;
+        const float4* pv = reinterpret_cast<const float4*>(dots + (4 * r + k) * kStride);
+        const float4* sv = reinterpret_cast<const float4*>(dots + (4 * kRows + r) * kStride);
+        float a = c == 0 ? 0.0f : acc;
+        int q = 0;
+        const int n4 = cn >> 2;
+        for (; q + 7 < n4; q += 8) {  // 32 blocks a batch: 16 reads issued before the first FMA
+            float4 vv[8], ss[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                vv[i] = pv[q + i];
+                ss[i] = sv[q + i];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                a = fmaf(vv[i].x, ss[i].x, a);
+                a = fmaf(vv[i].y, ss[i].y, a);
+                a = fmaf(vv[i].z, ss[i].z, a);
+                a = fmaf(vv[i].w, ss[i].w, a);
+            }
+        }
+        for (; q + 1 < n4; q += 2) {  // cn % 8 == 0: whole pairs of float4
+            const float4 v0 = pv[q], v1 = pv[q + 1], s0 = sv[q], s1 = sv[q + 1];
+            a = fmaf(v0.x, s0.x, a);
+            a = fmaf(v0.y, s0.y, a);
+            a = fmaf(v0.z, s0.z, a);
+            a = fmaf(v0.w, s0.w, a);
+            a = fmaf(v1.x, s1.x, a);
+            a = fmaf(v1.y, s1.y, a);
+            a = fmaf(v1.z, s1.z, a);
+            a = fmaf(v1.w, s1.w, a);
+        }
+        acc = a;
+        if (c == chunks - 1) {
+            a = a + dpp_f<kDppQuadXor2>(a);  // lanes k and k + 2
+            a = a + dpp_f<kDppQuadXor1>(a);  // then the two pair sums
+            const int lr = g * kRows + r, row = row0 + lr;
+            if (silu_pairs) {
+                // Rows 2n and 2n + 1 are gate_n and up_n (row0 and kRows even): y[n] = silu(gate) * up.
+                const float up = __shfl_xor(a, 4, kWave);
+                if (k == 0 && (r & 1) == 0 && row < row_end) y[row >> 1] = bad[0] ? __builtin_nanf("") : silu_ref(a) * up;
+            } else if (k == 0 && row < row_end) {
+                y[row] = bad[0] ? __builtin_nanf("") : (accumulate ? y_prev[lr] + a : a);
+            }
+        }
+    };
+
+    // x first (its own loads, every wave's ahead of any weight load), then the first TF tiles,
+    // then x is quantized while they are in flight.
+    XPreload<kThreads, PQ, 1> xpre;
+    xpre.load(x, K, 1, K);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    Slot ring[TF];
+#pragma unroll
+    for (int s = 0; s < TF; ++s) load_tile(s, ring[s]);
+    __builtin_amdgcn_sched_barrier(0);
+    xpre.template quantize<true, false, true>(x, K, 1, K, lds_q, lds_cb, lds_dx, bad);
+    lds_barrier();
+    // The dot lanes' x data, for the chunks a row has (held in registers when XR > 0).
+    constexpr int kXr = XR > 0 ? XR : 1;
+    XPair xr[kXr];
+    if (XR > 0 && wave != kChainWave) {
+#pragma unroll
+        for (int c = 0; c < kXr; ++c) xr[c] = read_x_pair(lds_q, lds_cb, lds_dx, pairs, min(c * 32 + p1, pairs - 1));
+    }
+    // The chain wave's FMA chains are the critical path of a step (each FMA waits for the one
+    // before it): it takes issue priority over the dot waves that share its SIMD.
+    if (wave == kChainWave) __builtin_amdgcn_s_setprio(3);
+
+    // Step t: stage tile t and issue tile t + TF's loads; barrier; phase 1 of tile t (dot waves)
+    // beside phase 2 of tile t - 1 (chain wave).
+    const int steps = (T + 1 + TF - 1) / TF * TF;  // every tile's phase 2 runs inside the loop
+    for (int t0 = 0; t0 < steps; t0 += TF) {
+#pragma unroll
+        for (int s = 0; s < TF; ++s) {
+            const int t = t0 + s;
+            if (t < T) stage_tile(t, ring[s]);
+            load_tile(t + TF, ring[s]);
+            lds_barrier();
+            if (wave == kChainWave) {
+                if (t >= 1 && t - 1 < T) phase2(t - 1);
+            } else if (t < T) {
+                if constexpr (XR > 0) {
+                    phase1(t, xr[s % kXr]);  // t0 is a multiple of TF, so chunk(t) = s % XR
+                } else {
+                    const int c = t % chunks;
+                    phase1(t, read_x_pair(lds_q, lds_cb, lds_dx, pairs, min(c * 32 + p1, pairs - 1)));
+                }
+            }
+        }
+    }
+}
+
 // Odd K/32 or a 2-byte aligned W: four lanes per row walk the blocks themselves (16-bit
 // loads), in the same order; 64 rows per 256-thread workgroup.
 template <int MT>
@@ -1149,6 +1417,57 @@ hipError_t launch_ordered_lpr(int lpr, int M, int N, int K, const float* x, int 
     }
 }
 
+// The tiled kernel (gemv_q4_tiled_kernel): 0 the built-in choice, -1 never, 2..4 that many
+// tiles in flight wherever the shape allows it (diagnostics).
+int g_q4_tiles = 0;
+
+size_t tiled_lds_bytes(int K, int rows_per_wg, int acc) {
+    return 4 * static_cast<size_t>(tiled_x_words(K)) + 2 * tiled::kPieces * 16 + 2 * tiled::kDotFloats * 4 +
+           (acc ? 4 * static_cast<size_t>(rows_per_wg) : 0);
+}
+
+// One row of x, N even, K/32 a multiple of 8 (rows of whole 16-byte pieces), W 16-byte aligned,
+// no fused norm, and the LDS image within 150 KiB (K up to about 37k).
+bool tiled_ok(int K, const uint8_t* W, int rows_per_wg, int acc) {
+    return g_q4_tiles >= 0 && (K >> 5) % 8 == 0 && reinterpret_cast<uintptr_t>(W) % 16 == 0 &&
+           tiled_lds_bytes(K, rows_per_wg, acc) <= 150 * 1024;
+}
+
+template <int TF, int PQ, int XR>
+hipError_t launch_tiled_kernel(int N, int K, const float* x, const uint8_t* W, float* y, int rpw, int acc, int silu,
+                               hipStream_t stream) {
+    const size_t lds = tiled_lds_bytes(K, rpw, acc);
+    if (const hipError_t e = allow_lds(gemv_q4_tiled_kernel<TF, PQ, XR>, lds); e != hipSuccess) return e;
+    const int grid = (N + rpw - 1) / rpw;
+    hipLaunchKernelGGL((gemv_q4_tiled_kernel<TF, PQ, XR>), dim3(grid), dim3(tiled::kThreads), lds, stream, N, K, x, W,
+                       y, rpw, acc, silu);
+    return hipGetLastError();
+}
+
+// x data in registers for rows of one or two chunks (K <= 4096), read from LDS otherwise.
+template <int TF>
+hipError_t launch_tiled_tf(int N, int K, const float* x, const uint8_t* W, float* y, int rpw, int acc, int silu,
+                           hipStream_t stream) {
+    const int chunks = ((K >> 5) + tiled::kBlocks - 1) / tiled::kBlocks;
+    const int pq = ((K >> 3) + tiled::kThreads - 1) / tiled::kThreads;  // octs of x per thread
+    if (chunks == 1) return launch_tiled_kernel<TF, 1, 1>(N, K, x, W, y, rpw, acc, silu, stream);
+    if constexpr (TF == 2)  // (two chunks in registers and four tiles in flight would spill)
+        if (chunks == 2) return launch_tiled_kernel<TF, 1, 2>(N, K, x, W, y, rpw, acc, silu, stream);
+    if (pq <= 1) return launch_tiled_kernel<TF, 1, 0>(N, K, x, W, y, rpw, acc, silu, stream);
+    if (pq <= 2) return launch_tiled_kernel<TF, 2, 0>(N, K, x, W, y, rpw, acc, silu, stream);
+    return launch_tiled_kernel<TF, 4, 0>(N, K, x, W, y, rpw, acc, silu, stream);  // octs past 4 a thread: loop
+}
+
+hipError_t launch_tiled(int N, int K, const float* x, const uint8_t* W, float* y, int rpw, int acc, int silu,
+                        hipStream_t stream) {
+    const int tf = g_q4_tiles >= 2 ? g_q4_tiles : 2;
+    switch (tf) {
+        case 3: return launch_tiled_tf<3>(N, K, x, W, y, rpw, acc, silu, stream);
+        case 4: return launch_tiled_tf<4>(N, K, x, W, y, rpw, acc, silu, stream);
+        default: return launch_tiled_tf<2>(N, K, x, W, y, rpw, acc, silu, stream);
+    }
+}
+
 template <int MT>
 hipError_t launch_ordered_generic(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
                                   int acc, hipStream_t stream) {
@@ -1217,6 +1536,15 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
     if (rpw <= 0) {
         rpw = std::max(1, (N + g_cus - 1) / g_cus);
         rpw += rpw & 1;  // (gate, up) pairs of the SiLU epilogue never straddle workgroups
+    }
+    // The K-chunk tiled kernel where it measured faster on MI355X (graph-replayed, us, tiled /
+    // row-group): long rows, 4096x14336 12.1 / 16.0; many rows a workgroup, 128256x4096 56.0 / 58.8.
+    // Short rows and few rows keep the row-group kernel (8192x2048 5.65 / 4.38, 14336x4096 11.0 /
+    // 10.4, 2048x8192 8.15 / 6.25): its one or two groups need fewer barriers.
+    const bool tiled_pays = g_q4_tiles > 0 || K >= 12288 || rpw >= 256;
+    if (mt == 1 && !nrm.w && !(t && (t->lanes_per_row || t->threads)) && tiled_pays && tiled_ok(K, W, rpw, acc) &&
+        !(nrm.silu_pairs && (rpw & 1))) {
+        return launch_tiled(N, K, x, W, y, rpw, acc, nrm.silu_pairs, stream);
     }
     if (mt == 1) {
         if (nrm.silu_pairs) {
@@ -1359,6 +1687,8 @@ const char* gemv_quant_path(int, int, int K, const uint8_t* W) { return pair_pat
 void set_compute_units(int cus) { g_cus = cus > 0 ? cus : 256; }
 
 void set_q4_stream(int mode) { g_q4_stream = mode; }
+
+void set_q4_tiles(int tiles) { g_q4_tiles = tiles; }
 
 hipError_t quantize_x_q8(int K, const float* x, int8_t* qs, float* dx, int* bad, hipStream_t stream) {
     if (K <= 0) return hipSuccess;

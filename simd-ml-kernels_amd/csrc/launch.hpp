@@ -62,6 +62,11 @@ void set_compute_units(int cus);
 // where the shape allows it).  Not synchronised with launches in flight.
 void set_q4_stream(int mode);
 
+// Diagnostics: the K-chunk tiled kernel of the reference-order Q4_0 GEMV for one row of x (0 the
+// built-in choice, -1 never, 2..4 that many tiles in flight wherever the shape allows it).  Not
+// synchronised with launches in flight.
+void set_q4_tiles(int tiles);
+
 // Diagnostics: lanes per row (16, 32 or 64; 0 automatic) and rows per lane group (2 or 4) of
 // the FP16 / BF16 / FP32 GEMV.
 void set_lowp_tuning(int lanes_per_row, int unroll);

@@ -140,16 +140,20 @@ struct PinBuf {
 
 std::atomic<bool> g_exiting{false};
 
+// Pinned staging: ha carries the first upload of a call (x or A), hb the second (C of a
+// product with beta != 0), hc the download.  Each buffer is reused only after the stream has
+// drained (every host-pointer call ends with a synchronizing download), so an upload still
+// queued on the stream never sees its staging bytes overwritten by a later one of the same call.
 struct Ctx {
     hipStream_t stream = nullptr;
     DevBuf a, b, c, w, flag;
-    PinBuf ha, hc;
+    PinBuf ha, hb, hc;
     ~Ctx() {
         if (g_exiting.load()) return;  // the runtime may already be gone at process exit
         if (stream) (void)hipStreamDestroy(stream);
         for (DevBuf* d : {&a, &b, &c, &w, &flag})
             if (d->p) (void)hipFree(d->p);
-        for (PinBuf* h : {&ha, &hc})
+        for (PinBuf* h : {&ha, &hb, &hc})
             if (h->p) (void)hipHostFree(h->p);
     }
 };
@@ -205,15 +209,17 @@ int weights_on_device(Ctx* c, const void* p, size_t n, const void** dev) {
     return SMK_OK;
 }
 
-// Small host -> device copy through pinned staging.
-int upload(Ctx* c, DevBuf& dst, const void* src, size_t n) {
+// Small host -> device copy through the pinned staging buffer `stage` (asynchronous: the
+// caller must not reuse `stage` in the same call before the stream has run the copy).
+int upload(Ctx* c, DevBuf& dst, const void* src, size_t n, PinBuf& stage) {
     SMK_HIP(dst.reserve(n), "device scratch");
     if (n == 0) return SMK_OK;
-    SMK_HIP(c->ha.reserve(n), "pinned staging");
-    std::memcpy(c->ha.p, src, n);
-    SMK_HIP(hipMemcpyAsync(dst.p, c->ha.p, n, hipMemcpyHostToDevice, c->stream), "upload");
+    SMK_HIP(stage.reserve(n), "pinned staging");
+    std::memcpy(stage.p, src, n);
+    SMK_HIP(hipMemcpyAsync(dst.p, stage.p, n, hipMemcpyHostToDevice, c->stream), "upload");
     return SMK_OK;
 }
+int upload(Ctx* c, DevBuf& dst, const void* src, size_t n) { return upload(c, dst, src, n, c->ha); }
 
 // Device -> host through pinned staging; waits for the stream.
 int download(Ctx* c, void* dst, const void* src, size_t n) {
@@ -305,7 +311,8 @@ int host_gemm(int elem, bool ta, bool tb, int M, int N, int K, float alpha, cons
         if (const int rc = weights_on_device(c, B, b_bytes, &bd)) return rc;
     }
     if (beta != 0.0f) {
-        if (const int rc = upload(c, c->c, C, c_bytes)) return rc;
+        // C through its own staging buffer: A's upload from ha may not have run yet.
+        if (const int rc = upload(c, c->c, C, c_bytes, c->hb)) return rc;
     } else {
         SMK_HIP(c->c.reserve(c_bytes), "device scratch");
     }
@@ -709,6 +716,13 @@ int smk_set_q4_order(int reference_order) {
 int smk_set_q4_stream(int mode) {
     if (mode < -1 || mode > 2) return fail(SMK_ERR_ARGUMENT, "mode must be -1, 0, 1 or 2");
     smk::set_q4_stream(mode);
+    return ok();
+}
+
+int smk_set_q4_tiles(int tiles_in_flight) {
+    if (tiles_in_flight != 0 && tiles_in_flight != -1 && (tiles_in_flight < 2 || tiles_in_flight > 4))
+        return fail(SMK_ERR_ARGUMENT, "tiles_in_flight must be -1, 0, 2, 3 or 4");
+    smk::set_q4_tiles(tiles_in_flight);
     return ok();
 }
 

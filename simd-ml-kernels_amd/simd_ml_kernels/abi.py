@@ -102,6 +102,7 @@ SIGNATURES = {
     "smk_set_gemv_tuning": [_i, _i, _i, _i],
     "smk_set_q4_order": [_i],
     "smk_set_q4_stream": [_i],
+    "smk_set_q4_tiles": [_i],
     "smk_set_q4_mfma_min_rows": [_i],
     "smk_gemv_path": [_i, _p],
 }

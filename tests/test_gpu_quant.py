@@ -214,6 +214,7 @@ class TestQ4ReferenceOrder:
         (smk_set_q4_stream): y bit-exact with the reference order in each form, at the decode
         shapes, config 1, a Llama-3-8B shape and uneven workgroups."""
         g.call("smk_set_q4_stream", mode)
+        g.call("smk_set_q4_tiles", -1)  # the row-group kernel, whose load forms these are
         try:
             for N, K in ((8192, 2048), (3072, 2048), (16384, 2048), (2048, 8192), (1000, 4096), (14336, 4096)):
                 x, wq = _inputs("q4_0", N, K, 7 * N + K + mode)
@@ -222,6 +223,44 @@ class TestQ4ReferenceOrder:
                                               err_msg=f"mode {mode} N={N} K={K}")
         finally:
             g.call("smk_set_q4_stream", -1)
+            g.call("smk_set_q4_tiles", 0)
+
+    # K-chunk tiles: full chunks (K % 2048 == 0), a partial last chunk (K/32 % 64 != 0), one
+    # partial chunk only (K = 256, 768), long rows (14336, 32768), uneven workgroups, and the
+    # Llama-3-8B / BASELINE shapes.
+    TILED = [(8192, 2048), (14336, 4096), (4096, 14336), (2048, 8192), (1000, 4096), (513, 2304), (40, 256),
+             (17, 768), (250, 11008), (64, 32768), (4098, 4096), (1, 4096), (31, 2048)]
+
+    @pytest.mark.parametrize("tiles", [2, 3, 4])
+    def test_tiled_kernel_every_depth_same_bits(self, tiles):
+        """The K-chunk tiled kernel (smk_set_q4_tiles), 2, 3 and 4 tiles in flight: y bit-exact
+        with the reference order at every shape of TILED (and so with the row-group kernel)."""
+        g.call("smk_set_q4_tiles", tiles)
+        try:
+            for N, K in self.TILED:
+                x, wq = _inputs("q4_0", N, K, 3 * N + K + tiles)
+                y = d_gemv("q4_0", x, wq, N, K)
+                np.testing.assert_array_equal(y.view(np.uint32), o.gemv_q4_0_simd(x, wq, N, K).view(np.uint32),
+                                              err_msg=f"tiles {tiles} N={N} K={K}")
+        finally:
+            g.call("smk_set_q4_tiles", 0)
+
+    def test_tiled_kernel_nonfinite_x_and_extremes(self):
+        """A NaN in x makes every y NaN; saturated quants (|x| at a block's max, nibbles 0 and 15)
+        keep the exact integer dots at their extremes; the tiled kernel against the reference order."""
+        N, K = 300, 4096
+        x, wq = _inputs("q4_0", N, K, 17)
+        wq = wq.copy()
+        blk = wq.reshape(N, K // 32, 18)
+        blk[::3, :, 2:] = 0xFF      # q = 15 everywhere
+        blk[1::3, :, 2:] = 0x00     # q = 0 everywhere
+        x[:32] = 127.0
+        x[32:64] = -127.0
+        y = d_gemv("q4_0", x, wq, N, K)
+        np.testing.assert_array_equal(y.view(np.uint32), o.gemv_q4_0_simd(x, wq, N, K).view(np.uint32))
+        x[4000] = np.nan
+        y = d_gemv("q4_0", x, wq, N, K)
+        assert np.isnan(y).all()
 
     @pytest.mark.parametrize("lpr", [8, 16, 32, 64])
     def test_lane_split_does_not_change_bits(self, lpr):
