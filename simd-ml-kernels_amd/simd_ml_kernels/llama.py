@@ -54,10 +54,9 @@ class Config:
 
     @classmethod
     def from_dict(cls, c: dict, generation: dict | None = None) -> "Config":
-        if c.get("model_type") != "llama":
-            raise ValueError(f"model_type {c.get('model_type')!r}: only 'llama' is supported")
-        if c.get("attention_bias") or c.get("mlp_bias") or c.get("hidden_act", "silu") != "silu":
-            raise ValueError("attention_bias / mlp_bias / non-SiLU activation are not implemented")
+        reason = _unsupported_architecture(c)
+        if reason:
+            raise ValueError(f"this decode engine runs Llama models only: {reason}")
         eos = (generation or {}).get("eos_token_id", c.get("eos_token_id"))
         eos_ids = tuple(eos) if isinstance(eos, list) else (() if eos is None else (int(eos),))
         heads = int(c["num_attention_heads"])
@@ -80,6 +79,19 @@ class Config:
             with open(gen_path) as f:
                 gen = json.load(f)
         return cls.from_dict(c, gen)
+
+
+def _unsupported_architecture(c: dict) -> str | None:
+    """Why a config.json describes a model the engine cannot run (None when it can): it must be
+    model_type "llama" with SiLU gating and no bias terms (the example's model, llama.py:73-123)."""
+    checks = (("model_type", c.get("model_type") == "llama", "model_type is {!r}"),
+              ("attention_bias", not c.get("attention_bias"), "attention_bias is {!r}"),
+              ("mlp_bias", not c.get("mlp_bias"), "mlp_bias is {!r}"),
+              ("hidden_act", c.get("hidden_act", "silu") == "silu", "hidden_act is {!r}"))
+    for key, ok, text in checks:
+        if not ok:
+            return text.format(c.get(key))
+    return None
 
 
 # Llama-3.2-1B's architecture (BASELINE config 5): the shape of the synthetic benchmark model.
@@ -147,7 +159,7 @@ class _Linear:
 
     def __init__(self, t: ggufmod.Tensor):
         if t.type not in _MATRIX_TYPES:
-            raise ValueError(f"{t.name} is {t.type_name}; F32, Q8_0 or Q4_0 expected")
+            raise ValueError(f"{t.name} is {ggufmod.type_label(t.type)}; F32, Q8_0 or Q4_0 expected")
         self.kind, self.data, self.shape = _MATRIX_TYPES[t.type], t.data, t.shape
         n, k = t.shape
         if self.kind == "q4_0":
@@ -198,7 +210,8 @@ class Llama:
         self._check_shapes()
         types: dict[str, int] = {}
         for t in T.values():
-            types[t.type_name] = types.get(t.type_name, 0) + 1
+            label = ggufmod.type_label(t.type)
+            types[label] = types.get(label, 0) + 1
         self.weight_types = types
         self.k_cache: np.ndarray | None = None
         self.v_cache: np.ndarray | None = None
@@ -515,30 +528,40 @@ def config_from_gguf(g: ggufmod.GGUF) -> Config:
                   tie_word_embeddings="output.weight" not in g.tensors)
 
 
+# GGUF metadata keys that must agree with the configuration, and the Config field each mirrors.
+_METADATA_FIELDS = (("llama.block_count", "num_hidden_layers"), ("llama.embedding_length", "hidden_size"),
+                    ("llama.feed_forward_length", "intermediate_size"),
+                    ("llama.attention.head_count", "num_attention_heads"),
+                    ("llama.attention.head_count_kv", "num_key_value_heads"))
+
+
 def _check_metadata(g: ggufmod.GGUF, cfg: Config, path: str) -> None:
+    """The file must be a Llama GGUF whose shape metadata (where present) matches `cfg`; every
+    disagreement is reported at once (the example's loader checks the same keys, llama.py:302-316)."""
     md = g.metadata
-    if md.get("general.architecture") != "llama":
-        raise ValueError(f"{path}: architecture {md.get('general.architecture')!r}, expected llama")
-    want = {"llama.block_count": cfg.num_hidden_layers, "llama.embedding_length": cfg.hidden_size,
-            "llama.feed_forward_length": cfg.intermediate_size,
-            "llama.attention.head_count": cfg.num_attention_heads,
-            "llama.attention.head_count_kv": cfg.num_key_value_heads}
-    for key, val in want.items():
-        if key in md and int(md[key]) != val:
-            raise ValueError(f"{path}: {key} = {md[key]}, the config says {val}")
+    arch = md.get("general.architecture")
+    problems = [] if arch == "llama" else [f"general.architecture is {arch!r}, not 'llama'"]
+    for key, field_name in _METADATA_FIELDS:
+        expected = getattr(cfg, field_name)
+        if key in md and int(md[key]) != expected:
+            problems.append(f"{key} is {md[key]} where the configuration has {field_name} = {expected}")
+    if problems:
+        raise ValueError(f"{path} does not match the model configuration: " + "; ".join(problems))
 
 
-GGUF_TYPES = {"fp32": "F32", "q8_0": "Q8_0", "q4_0": "Q4_0"}
+# Weight-type names of the example's command line and the file-name suffix of each GGUF.
+_GGUF_SUFFIX = {"fp32": "-F32.gguf", "q8_0": "-Q8_0.gguf", "q4_0": "-Q4_0.gguf"}
 
 
 def find_gguf(model_dir: str, weights: str) -> str:
-    """model_dir/gguf/*-<F32|Q8_0|Q4_0>.gguf (llama.py:508-517)."""
-    import glob
-
-    hits = sorted(glob.glob(os.path.join(model_dir, "gguf", f"*-{GGUF_TYPES[weights]}.gguf")))
-    if not hits:
-        raise FileNotFoundError(f"no {model_dir}/gguf/*-{GGUF_TYPES[weights]}.gguf")
-    return hits[0]
+    """The GGUF of weight type `weights` in <model_dir>/gguf: the first, in name order, whose name
+    ends with -F32 / -Q8_0 / -Q4_0 .gguf (the example's layout, llama.py:508-517)."""
+    folder = os.path.join(model_dir, "gguf")
+    suffix = _GGUF_SUFFIX[weights]
+    names = sorted(n for n in (os.listdir(folder) if os.path.isdir(folder) else []) if n.endswith(suffix))
+    if not names:
+        raise FileNotFoundError(f"{folder} holds no file ending in {suffix} (weights={weights!r})")
+    return os.path.join(folder, names[0])
 
 
 # ─── synthetic models ────────────────────────────────────────────────────────

@@ -57,8 +57,38 @@ class TestGGUF:
     def test_rejects_non_gguf_and_bad_type(self, tmp_path):
         p = tmp_path / "x.gguf"
         p.write_bytes(b"NOPE" + b"\0" * 64)
-        with pytest.raises(ValueError):
+        with pytest.raises(ValueError, match="magic"):
             gguf.GGUF(str(p))
+
+    def test_malformed_files(self, tmp_path):
+        """Version, value kind, truncation, unknown tensor type and a tensor past the end are all
+        refused with ValueError; string and numeric arrays are read."""
+        import struct
+
+        def header(n_tensors, pairs, version=3):
+            return b"GGUF" + struct.pack("<IQQ", version, n_tensors, len(pairs)) + b"".join(pairs)
+
+        def key(k):
+            return struct.pack("<Q", len(k)) + k.encode()
+
+        cases = {
+            "v1.gguf": (header(0, [], version=1), "version 1"),
+            "kind.gguf": (header(0, [key("a") + struct.pack("<I", 13) + b"\0" * 8]), "kind 13"),
+            "short.gguf": (header(0, [key("a") + struct.pack("<IQ", 8, 100) + b"xy"]), "truncated"),
+            "type.gguf": (header(1, []) + key("t") + struct.pack("<IQIQ", 1, 32, 6, 0) + b"\0" * 64, "ggml type 6"),
+            "past.gguf": (header(1, []) + key("t") + struct.pack("<IQIQ", 1, 4096, 0, 0) + b"\0" * 64, "needs bytes"),
+        }
+        for name, (blob, msg) in cases.items():
+            p = tmp_path / name
+            p.write_bytes(blob)
+            with pytest.raises(ValueError, match=msg):
+                gguf.GGUF(str(p))
+        names = key("names") + struct.pack("<IIQ", 9, 8, 2) + struct.pack("<Q", 2) + b"ab" + struct.pack("<Q", 1) + b"c"
+        ids = key("ids") + struct.pack("<IIQ", 9, 5, 3) + struct.pack("<3i", 7, -1, 9)
+        p = tmp_path / "arr.gguf"
+        p.write_bytes(header(0, [names, ids]))
+        g = gguf.GGUF(str(p))
+        assert g.metadata["names"] == ["ab", "c"] and list(g.metadata["ids"]) == [7, -1, 9]
 
 
 class TestSyntheticRecipe:
