@@ -14,11 +14,16 @@ namespace smk {
 
 // Allow `bytes` of dynamic LDS for `kernel` (above 64 KiB a launch needs the attribute; a
 // gfx950 CU has 160 KiB).
+// A refused request is returned and also cleared from the thread's last-error state: the
+// launchers report a launch's status through hipGetLastError(), which would otherwise return
+// this stale error for the next, valid launch.
 template <class Kernel>
 inline hipError_t allow_lds(Kernel kernel, size_t bytes) {
     if (bytes <= 65536) return hipSuccess;
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               static_cast<int>(bytes));
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    if (e != hipSuccess) (void)hipGetLastError();
+    return e;
 }
 
 constexpr int kWave = 64;

@@ -48,6 +48,9 @@
 
 #include <algorithm>
 #include <map>
+#include <thread>
+#include <tuple>
+#include <vector>
 #include <mutex>
 #include <utility>
 
@@ -464,31 +467,36 @@ size_t gemm_q4_mfma_workspace(int M, int K) {
     return best;
 }
 
-// Scratch of the batched path, one buffer per (device, stream): launches on one stream run in
-// order, so a buffer is never used by two products at once.  A buffer only grows, after its
-// stream has drained (never while the stream is being captured into a graph), and lives until
-// the process ends.
+// Scratch of the batched path, one buffer per (device, stream, host thread): launches on one
+// stream from one thread run in order, so a buffer is never used by two products at once, and
+// two threads sharing a stream (the null stream, say) get buffers of their own.  A buffer only
+// grows, outside stream capture; the buffer it replaces is never freed (a graph captured earlier
+// on that stream holds its address in its nodes and may be replayed later), so every buffer this
+// function hands out stays valid until the process ends.
 hipError_t stream_workspace(hipStream_t stream, size_t bytes, void** out) {
+    struct Slot {
+        void* p = nullptr;
+        size_t cap = 0;
+    };
     static std::mutex mu;
-    static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> cache;
+    static std::map<std::tuple<int, hipStream_t, std::thread::id>, Slot> cache;
+    static std::vector<void*> retired;  // superseded buffers, kept alive for captured graphs
     int dev = 0;
     if (const hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
     std::lock_guard<std::mutex> lk(mu);
-    auto& slot = cache[{dev, stream}];
-    if (slot.second < bytes) {
+    Slot& slot = cache[{dev, stream, std::this_thread::get_id()}];
+    if (slot.cap < bytes) {
         hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
         if (const hipError_t e = hipStreamIsCapturing(stream, &st); e != hipSuccess) return e;
         if (st != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
-        if (slot.first) {
-            if (const hipError_t e = hipStreamSynchronize(stream); e != hipSuccess) return e;
-            if (const hipError_t e = hipFree(slot.first); e != hipSuccess) return e;
-            slot = {nullptr, 0};
-        }
         const size_t grown = std::max(bytes, static_cast<size_t>(1) << 20);
-        if (const hipError_t e = hipMalloc(&slot.first, grown); e != hipSuccess) return e;
-        slot.second = grown;
+        void* p = nullptr;
+        if (const hipError_t e = hipMalloc(&p, grown); e != hipSuccess) return e;
+        if (slot.p) retired.push_back(slot.p);
+        slot.p = p;
+        slot.cap = grown;
     }
-    *out = slot.first;
+    *out = slot.p;
     return hipSuccess;
 }
 

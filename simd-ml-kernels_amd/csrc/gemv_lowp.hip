@@ -12,12 +12,14 @@
 #include "launch.hpp"
 
 #include <algorithm>
+#include <atomic>
 
 namespace smk {
 namespace {
 
 constexpr int kThreads = 256;
-int g_lowp_lpr = 0, g_lowp_unroll = 0;
+// Diagnostics settings (set_lowp_tuning), read by every launch.
+std::atomic<int> g_lowp_lpr{0}, g_lowp_unroll{0};
 
 template <int E>
 __device__ __forceinline__ float elem_to_float(const void* base, size_t i) {

@@ -34,6 +34,7 @@
 #include "pairwise_sum.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <type_traits>
 
@@ -1242,7 +1243,7 @@ __global__ void block_sums_kernel(int N, int K, const int8_t* __restrict__ qs, c
 // ─── host side ───────────────────────────────────────────────────────────────
 
 // Compute units of the device in use (set by the runtime at initialisation).
-int g_cus = 256;
+std::atomic<int> g_cus{256};
 
 bool pair_path_ok(int K, const uint8_t* W) {
     return ((K >> 5) % 2 == 0) && (reinterpret_cast<uintptr_t>(W) % 4 == 0);
@@ -1345,10 +1346,10 @@ hipError_t launch_ordered_kernel(int M, int N, int K, const float* x, int ldx, c
 // Streamed weight groups (kStream of gemv_q4_ordered_kernel): SMK_Q4_STREAM=0 pair loads,
 // 1 one group ahead, 2 two groups ahead (diagnostics, also set_q4_stream); unset: the built-in
 // choice (-1).
-int g_q4_stream = [] {
+std::atomic<int> g_q4_stream{[] {
     const char* v = std::getenv("SMK_Q4_STREAM");
     return v && v[0] >= '0' && v[0] <= '2' ? v[0] - '0' : -1;
-}();
+}()};
 
 template <int LPR, int MT, int NT, int CH>
 hipError_t launch_ordered_ch(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
@@ -1380,7 +1381,8 @@ hipError_t launch_ordered_ch(int M, int N, int K, const float* x, int ldx, const
         // ahead is faster (1,557 / 1,616 tok/s with every GEMV in one mode): the non-temporal
         // weights leave the activations and the KV cache in the caches.
         const int groups = (rows_per_wg + kRows - 1) / kRows;
-        const int mode = !st ? 0 : g_q4_stream > 0 ? g_q4_stream : groups >= 8 ? 2 : nrm.stream ? 1 : 0;
+        const int forced = g_q4_stream.load();
+        const int mode = !st ? 0 : forced > 0 ? forced : groups >= 8 ? 2 : nrm.stream ? 1 : 0;
 #define SMK_ORDERED(S, NORM) \
     launch_ordered_kernel<LPR, MT, NT, CH, S, NORM>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, nbuf, bytes, stream)
         if (nrm.w) return mode == 2 ? SMK_ORDERED(2, true) : mode == 1 ? SMK_ORDERED(1, true) : SMK_ORDERED(0, true);
@@ -1419,7 +1421,7 @@ hipError_t launch_ordered_lpr(int lpr, int M, int N, int K, const float* x, int 
 
 // The tiled kernel (gemv_q4_tiled_kernel): 0 the built-in choice, -1 never, 2..4 that many
 // tiles in flight wherever the shape allows it (diagnostics).
-int g_q4_tiles = 0;
+std::atomic<int> g_q4_tiles{0};
 
 size_t tiled_lds_bytes(int K, int rows_per_wg, int acc) {
     return 4 * static_cast<size_t>(tiled_x_words(K)) + 2 * tiled::kPieces * 16 + 2 * tiled::kDotFloats * 4 +
@@ -1460,7 +1462,8 @@ hipError_t launch_tiled_tf(int N, int K, const float* x, const uint8_t* W, float
 
 hipError_t launch_tiled(int N, int K, const float* x, const uint8_t* W, float* y, int rpw, int acc, int silu,
                         hipStream_t stream) {
-    const int tf = g_q4_tiles >= 2 ? g_q4_tiles : 2;
+    const int forced = g_q4_tiles.load();
+    const int tf = forced >= 2 ? forced : 2;
     switch (tf) {
         case 3: return launch_tiled_tf<3>(N, K, x, W, y, rpw, acc, silu, stream);
         case 4: return launch_tiled_tf<4>(N, K, x, W, y, rpw, acc, silu, stream);

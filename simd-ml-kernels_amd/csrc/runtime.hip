@@ -20,6 +20,7 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <shared_mutex>
 #include <string>
 
 namespace smk::abi {
@@ -95,6 +96,9 @@ Device& device() {
 int use_device() {
     Device& d = device();
     if (d.status != SMK_OK) return fail(d.status, d.error);
+    // Every entry point starts here: drop a stale error a failed call left in this thread's HIP
+    // state, so that the launches of this call report their own status only.
+    (void)hipGetLastError();
     int cur = -1;
     if (hipGetDevice(&cur) != hipSuccess || cur != d.id) SMK_HIP(hipSetDevice(d.id), "hipSetDevice");
     return SMK_OK;
@@ -178,13 +182,17 @@ struct Entry {
     void* dev = nullptr;
 };
 
-std::mutex g_cache_mu;
+// The weight cache.  Host-pointer calls hold g_cache_rw shared from their lookup until their
+// result is downloaded (the device is done with the copy by then); pinning, replacing and
+// unpinning take it exclusively, so a device copy is never freed under a call that uses it.
+std::shared_mutex g_cache_rw;
 std::map<uintptr_t, Entry> g_cache;  // keyed by host start address
 size_t g_cache_bytes = 0;
+using CacheUse = std::shared_lock<std::shared_mutex>;
 
-// Device address of host range [p, p + n) if a pinned entry covers it, else nullptr.
+// Device address of host range [p, p + n) if a pinned entry covers it, else nullptr.  The caller
+// holds a CacheUse.
 const void* cache_lookup(const void* p, size_t n) {
-    std::lock_guard<std::mutex> lk(g_cache_mu);
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
     auto it = g_cache.upper_bound(a);
     if (it == g_cache.begin()) return nullptr;
@@ -234,7 +242,31 @@ int download(Ctx* c, void* dst, const void* src, size_t n) {
     return SMK_OK;
 }
 
+// Diagnostics settings of the quantized GEMV (smk_set_*): written under g_tuning_mu, read as a
+// snapshot by every launch, so a setter running beside calls in flight never tears a read.
+std::mutex g_tuning_mu;
 smk::GemvTuning g_tuning;
+
+smk::GemvTuning tuning_now() {
+    std::lock_guard<std::mutex> lk(g_tuning_mu);
+    return g_tuning;
+}
+
+bool tuning_forced(const smk::GemvTuning& t) { return t.lanes_per_row || t.rows_per_wg || t.threads || t.unroll; }
+
+// A launch refused under forced diagnostics settings: the settings do not fit this shape (LDS,
+// lanes, rows) -- say so rather than report a bare launch error.  Out-of-memory keeps its code.
+int gemv_launch_fail(hipError_t e, const smk::GemvTuning& t, int M, int N, int K) {
+    if (e != hipErrorOutOfMemory && e != hipErrorMemoryAllocation && tuning_forced(t))
+        return fail(SMK_ERR_ARGUMENT, std::string("gemv launch (") + hipGetErrorString(e) +
+                                          "): the forced tuning (lanes_per_row " + std::to_string(t.lanes_per_row) +
+                                          ", rows_per_wg " + std::to_string(t.rows_per_wg) + ", threads " +
+                                          std::to_string(t.threads) + ", unroll " + std::to_string(t.unroll) +
+                                          ") does not fit M=" + std::to_string(M) + " N=" + std::to_string(N) +
+                                          " K=" + std::to_string(K) + "; smk_set_gemv_tuning(0, 0, 0, 0) restores "
+                                          "the built-in choice");
+    return hip_fail(e, "gemv launch");
+}
 
 int check_gemv_args(int M, int N, int K, const void* x, const void* W, const void* y) {
     if (M < 0 || N < 0 || K < 0) return fail(SMK_ERR_ARGUMENT, "M, N and K must be >= 0");
@@ -253,16 +285,20 @@ int host_gemm_quant(int bb, int M, int N, int K, const float* X, const uint8_t* 
     }
     Ctx* c;
     if (const int rc = context(&c)) return rc;
+    CacheUse use(g_cache_rw);
     const void* wd;
     if (const int rc = weights_on_device(c, Wq, static_cast<size_t>(N) * (K / 32) * bb, &wd)) return rc;
+    const smk::GemvTuning tuning = tuning_now();
     // Rows of X in uploads of at most 32 (one matrix-core launch at K <= 4096).
     for (int m0 = 0; m0 < M; m0 += 32) {
         const int mr = std::min(32, M - m0);
         if (const int rc = upload(c, c->a, X + static_cast<size_t>(m0) * K, static_cast<size_t>(mr) * K * 4)) return rc;
         SMK_HIP(c->c.reserve(static_cast<size_t>(mr) * N * 4), "device scratch");
-        SMK_HIP(smk::gemv_quant(bb, mr, N, K, static_cast<const float*>(c->a.p), K, static_cast<const uint8_t*>(wd),
-                                static_cast<float*>(c->c.p), N, c->stream, &g_tuning),
-                "gemv launch");
+        if (const hipError_t e = smk::gemv_quant(bb, mr, N, K, static_cast<const float*>(c->a.p), K,
+                                                 static_cast<const uint8_t*>(wd), static_cast<float*>(c->c.p), N,
+                                                 c->stream, &tuning);
+            e != hipSuccess)
+            return gemv_launch_fail(e, tuning, mr, N, K);
         if (const int rc = download(c, Y + static_cast<size_t>(m0) * N, c->c.p, static_cast<size_t>(mr) * N * 4))
             return rc;
     }
@@ -303,6 +339,7 @@ int host_gemm(int elem, bool ta, bool tb, int M, int N, int K, float alpha, cons
     const size_t a_bytes = a_rows ? ((a_rows - 1) * lda + (ta ? M : K)) * es : 0;
     const size_t b_bytes = b_rows ? ((b_rows - 1) * ldb + (tb ? K : N)) * es : 0;
     const size_t c_bytes = ((static_cast<size_t>(M) - 1) * ldc + N) * 4;
+    CacheUse use(g_cache_rw);
     if (K > 0) {
         if (const int rc = upload(c, c->a, A, a_bytes)) return rc;
     }
@@ -406,6 +443,7 @@ int smk_rms_norm(const float* x, const float* w, float* y, int rows, int n, doub
     Ctx* c;
     if (const int rc = context(&c)) return rc;
     const size_t bytes = static_cast<size_t>(rows) * n * 4;
+    CacheUse use(g_cache_rw);
     if (const int rc = upload(c, c->a, x, bytes)) return rc;
     const void* wd;
     if (const int rc = weights_on_device(c, w, static_cast<size_t>(n) * 4, &wd)) return rc;
@@ -443,7 +481,7 @@ int smk_weights_pin(const void* host, size_t nbytes) {
     if (!host || nbytes == 0) return fail(SMK_ERR_ARGUMENT, "pin: empty range");
     if (const int rc = use_device()) return rc;
     {
-        std::lock_guard<std::mutex> lk(g_cache_mu);
+        CacheUse use(g_cache_rw);
         auto it = g_cache.find(reinterpret_cast<uintptr_t>(host));
         if (it != g_cache.end() && it->second.bytes >= nbytes) return ok();
     }
@@ -454,9 +492,9 @@ int smk_weights_pin(const void* host, size_t nbytes) {
         (void)hipFree(dev);
         return hip_fail(e, "pin: upload");
     }
-    std::lock_guard<std::mutex> lk(g_cache_mu);
+    std::unique_lock<std::shared_mutex> lk(g_cache_rw);  // waits for the calls using the cache
     auto it = g_cache.find(reinterpret_cast<uintptr_t>(host));
-    if (it != g_cache.end()) {  // replaced by a larger range: the old copy may be in use
+    if (it != g_cache.end()) {  // replaced by a larger range: device-pointer work may still read it
         (void)hipDeviceSynchronize();
         (void)hipFree(it->second.dev);
         g_cache_bytes -= it->second.bytes;
@@ -469,7 +507,7 @@ int smk_weights_pin(const void* host, size_t nbytes) {
 
 int smk_weights_unpin(const void* host) {
     if (const int rc = use_device()) return rc;
-    std::lock_guard<std::mutex> lk(g_cache_mu);
+    std::unique_lock<std::shared_mutex> lk(g_cache_rw);  // waits for the calls using the cache
     auto it = g_cache.find(reinterpret_cast<uintptr_t>(host));
     if (it == g_cache.end()) return ok();
     SMK_HIP(hipDeviceSynchronize(), "unpin: synchronize");
@@ -480,7 +518,7 @@ int smk_weights_unpin(const void* host) {
 }
 
 int smk_weights_stats(size_t* bytes, int* entries) {
-    std::lock_guard<std::mutex> lk(g_cache_mu);
+    CacheUse use(g_cache_rw);
     if (bytes) *bytes = g_cache_bytes;
     if (entries) *entries = static_cast<int>(g_cache.size());
     return ok();
@@ -497,7 +535,9 @@ static int d_gemm_quant(int bb, int M, int N, int K, const float* X, int ldx, co
     if (reinterpret_cast<uintptr_t>(X) % 4 || reinterpret_cast<uintptr_t>(Wq) % 2 || reinterpret_cast<uintptr_t>(Y) % 4)
         return fail(SMK_ERR_ARGUMENT, "X and Y must be 4-byte aligned and Wq 2-byte aligned");
     if (const int rc = use_device()) return rc;
-    SMK_HIP(smk::gemv_quant(bb, M, N, K, X, ldx, Wq, Y, ldy, S(stream), &g_tuning), "gemv launch");
+    const smk::GemvTuning tuning = tuning_now();
+    if (const hipError_t e = smk::gemv_quant(bb, M, N, K, X, ldx, Wq, Y, ldy, S(stream), &tuning); e != hipSuccess)
+        return gemv_launch_fail(e, tuning, M, N, K);
     return ok();
 }
 
@@ -709,6 +749,7 @@ int smk_runtime_version(int* runtime, int* built) {
 
 int smk_set_q4_order(int reference_order) {
     if (reference_order != 0 && reference_order != 1) return fail(SMK_ERR_ARGUMENT, "reference_order must be 0 or 1");
+    std::lock_guard<std::mutex> lk(g_tuning_mu);
     g_tuning.unordered = reference_order ? 0 : 1;
     return ok();
 }
@@ -728,6 +769,7 @@ int smk_set_q4_tiles(int tiles_in_flight) {
 
 int smk_set_q4_mfma_min_rows(int rows) {
     if (rows < 0) return fail(SMK_ERR_ARGUMENT, "rows must be >= 0");
+    std::lock_guard<std::mutex> lk(g_tuning_mu);
     g_tuning.mfma_min_rows = rows;
     return ok();
 }
@@ -739,6 +781,7 @@ int smk_set_gemv_tuning(int lanes_per_row, int rows_per_wg, int threads, int unr
     if (threads != 0 && threads != 256 && threads != 512 && threads != 1024)
         return fail(SMK_ERR_ARGUMENT, "threads must be 0, 256, 512 or 1024");
     if (unroll != 0 && unroll != 1 && unroll != 2 && unroll != 4) return fail(SMK_ERR_ARGUMENT, "unroll must be 0, 1, 2 or 4");
+    std::lock_guard<std::mutex> lk(g_tuning_mu);
     g_tuning.lanes_per_row = lanes_per_row;
     g_tuning.rows_per_wg = rows_per_wg;
     g_tuning.threads = threads;

@@ -511,10 +511,11 @@ PYBIND11_MODULE(_core, m) {
           py::arg("isa"), "Make this kernel table the active one (private; the selftest's loop).");
     m.def("_pin", [](py::array a) {
               const void* p = a.data();
+              const size_t n = static_cast<size_t>(a.nbytes());  // (Python API: read with the GIL held)
               int rc;
               {
                   py::gil_scoped_release release;
-                  rc = smk_weights_pin(p, static_cast<size_t>(a.nbytes()));
+                  rc = smk_weights_pin(p, n);
               }
               smk_host::check(rc, "pin");
               std::lock_guard<std::mutex> lk(g_pin_mu);
@@ -522,7 +523,13 @@ PYBIND11_MODULE(_core, m) {
           },
           py::arg("arr"), "Keep a device copy of arr for later calls (benchmarks). The caller must not modify arr.");
     m.def("_unpin", [](py::array a) {
-              smk_host::check(smk_weights_unpin(a.data()), "unpin");
+              const void* p = a.data();
+              int rc;
+              {
+                  py::gil_scoped_release release;  // waits for the calls that use the cached copy
+                  rc = smk_weights_unpin(p);
+              }
+              smk_host::check(rc, "unpin");
               std::lock_guard<std::mutex> lk(g_pin_mu);
               g_pinned.erase(a.data());
           },

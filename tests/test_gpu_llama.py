@@ -87,6 +87,34 @@ def test_tiny_long_context_several_attention_rounds(tmp_path):
         m.close()
 
 
+@pytest.mark.parametrize("head_dim,heads,kv_heads", [(128, 4, 2), (256, 2, 1)])
+def test_wide_heads_several_attention_rounds(tmp_path, head_dim, heads, kv_heads):
+    """head_dim 128 (Llama-3-8B) and 256 (the engine's limit): the attention kernel's K / V tiles
+    then hold fewer positions than at head_dim 64, so a 400-position cache takes several rounds.
+    Logits bit-identical with the reference loop at positions across every round."""
+    cfg = dict(TINY, hidden_size=heads * head_dim, intermediate_size=2 * heads * head_dim,
+               num_attention_heads=heads, num_key_value_heads=kv_heads, head_dim=head_dim)
+    path, prompt = llama.write_synthetic_model(str(tmp_path), cfg, seed=31 + head_dim, n_prompt=8,
+                                               weight_type=gguf.Q4_0)
+    c = lr.Cfg.from_config(cfg)
+    oprompt, W = lr.synthetic_model(c, 31 + head_dim, 8, lr.Q4_0)
+    assert prompt == oprompt
+    dec = lr.Decoder(c, W, lr.Q4_0, _oracle_kind())
+    rng = np.random.default_rng(head_dim)
+    seq = prompt + [int(t) for t in rng.integers(0, cfg["vocab_size"], 392)]
+    m = llama.Llama(str(tmp_path), gguf=path)
+    try:
+        m.reset(len(seq))
+        dec.reset(len(seq))
+        for i, t in enumerate(seq):
+            lg = m.step(t)
+            lo = dec.step(t)
+            if i % 23 == 0 or i >= len(seq) - 3:
+                np.testing.assert_array_equal(lg.view(np.uint32), lo.view(np.uint32), err_msg=f"position {i}")
+    finally:
+        m.close()
+
+
 MID = dict(TINY, hidden_size=2048, intermediate_size=8192, num_attention_heads=32, num_key_value_heads=8,
            head_dim=64)
 
