@@ -93,9 +93,18 @@ int smk_d_gemv_q4_0(int N, int K, const float* x, const uint8_t* Wq, float* y, v
 int smk_d_gemv_q8_0(int N, int K, const float* x, const uint8_t* Wq, float* y, void* stream);
 /* Rows m < M of X [M, ldx] against the same W: Y [M, ldy]; row m of Y equals the one-row call
  * on row m of X bit for bit.  Q4_0 with M >= 2 (K % 64 == 0) runs on the matrix cores, with a
- * scratch buffer the library keeps per stream (allocated on a stream's first call of a larger
- * size; that call must not be made while the stream is captured into a graph). */
+ * scratch buffer the library keeps per (stream, host thread): allocated on the first call of a
+ * larger size, which must not be made while the stream is captured into a graph; a buffer it
+ * replaces stays allocated until the process ends, so graphs captured earlier stay valid. */
 int smk_d_gemm_q4_0(int M, int N, int K, const float* X, int ldx, const uint8_t* Wq, float* Y, int ldy, void* stream);
+/* No reference counterpart: for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  smk_d_gemm_q4_0 -- the same
+ * kernels, the same bits -- with its scratch in a fixed 4 MiB array of the library (one per GPU,
+ * held until the process ends) instead of an allocated buffer; it allocates nothing.  Calls whose
+ * x image needs more (about M > 256 rows at K = 14336) are refused with SMK_ERR_ARGUMENT.  All
+ * calls on one GPU share the array: calls that overlap on one GPU race (serialize them). */
+int smk_d_gemm_q4_0_noalloc(int M, int N, int K, const float* X, int ldx, const uint8_t* Wq, float* Y, int ldy,
+                            void* stream);
 int smk_d_gemm_q8_0(int M, int N, int K, const float* X, int ldx, const uint8_t* Wq, float* Y, int ldy, void* stream);
 /* elem: 0 FP32, 1 FP16, 2 BF16.  C = beta C + alpha A B^T, A [M, lda], B [N, ldb]. */
 int smk_d_gemm_tb(int elem, int M, int N, int K, float alpha, const void* A, int lda, const void* B, int ldb,

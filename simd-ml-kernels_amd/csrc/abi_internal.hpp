@@ -14,6 +14,14 @@ int ok();                                     // clears the thread's error, retu
 int fail(int code, const std::string& msg);   // records msg, returns code
 int hip_fail(hipError_t e, const char* what); // maps a HIP error to SMK_ERR_DEVICE / _OUT_OF_MEMORY
 int use_device();                             // selects the library's device on this thread
+}  // namespace smk::abi
+
+#include "launch.hpp"
+
+namespace smk::abi {
+smk::GemvTuning tuning_snapshot();            // the diagnostics settings (smk_set_*) now in force
+int check_gemv_args(int M, int N, int K, const void* x, const void* W, const void* y);
+int gemv_launch_fail(hipError_t e, const smk::GemvTuning& t, int M, int N, int K);
 
 }  // namespace smk::abi
 

@@ -1660,8 +1660,13 @@ hipError_t gemv_quant(int block_bytes, int M, int N, int K, const float* x, int 
         const int ne = N & ~1;
         if (ne > 0 && gemm_q4_mfma_ok(M, ne, K, W)) {
             void* ws = nullptr;
-            if (const hipError_t e = stream_workspace(stream, gemm_q4_mfma_workspace(M, K), &ws); e != hipSuccess)
+            if (tuning && tuning->workspace) {  // the caller's scratch: never allocate
+                if (gemm_q4_mfma_workspace(M, K) > tuning->workspace_bytes) return hipErrorInvalidValue;
+                ws = tuning->workspace;
+            } else if (const hipError_t e = stream_workspace(stream, gemm_q4_mfma_workspace(M, K), &ws);
+                       e != hipSuccess) {
                 return e;
+            }
             const hipError_t e = gemm_q4_mfma(M, ne, K, x, ldx, W, y, ldy, tuning ? tuning->accumulate : 0, ws, stream);
             if (e != hipSuccess || ne == N) return e;
             const size_t row_bytes = static_cast<size_t>(K >> 5) * kQ4_0Bytes;

@@ -30,6 +30,8 @@ struct GemvTuning {
     int stream_weights = 0;         // Q4_0, one row of x: 1 streams the weights with
                                     // non-temporal loads wherever the shape allows (a decode
                                     // step: the caches keep its activations and KV cache)
+    void* workspace = nullptr;      // scratch of the batched Q4_0 path supplied by the caller
+    size_t workspace_bytes = 0;     // (instead of the stream's buffer): its size in bytes
 };
 
 // y[m*ldy + n] = sum_k x[m*ldx + k] * W[n][k] for m < M, W in GGUF Q4_0 (block_bytes 18) or

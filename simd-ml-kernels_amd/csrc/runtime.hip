@@ -104,6 +104,39 @@ int use_device() {
     return SMK_OK;
 }
 
+// Diagnostics settings of the quantized GEMV (smk_set_*): written under g_tuning_mu, read as a
+// snapshot by every launch, so a setter running beside calls in flight never tears a read.
+std::mutex g_tuning_mu;
+smk::GemvTuning g_tuning;
+
+smk::GemvTuning tuning_snapshot() {
+    std::lock_guard<std::mutex> lk(g_tuning_mu);
+    return g_tuning;
+}
+
+bool tuning_forced(const smk::GemvTuning& t) { return t.lanes_per_row || t.rows_per_wg || t.threads || t.unroll; }
+
+// A launch refused under forced diagnostics settings: the settings do not fit this shape (LDS,
+// lanes, rows) -- say so rather than report a bare launch error.  Out-of-memory keeps its code.
+int gemv_launch_fail(hipError_t e, const smk::GemvTuning& t, int M, int N, int K) {
+    if (e != hipErrorOutOfMemory && e != hipErrorMemoryAllocation && tuning_forced(t))
+        return fail(SMK_ERR_ARGUMENT, std::string("gemv launch (") + hipGetErrorString(e) +
+                                          "): the forced tuning (lanes_per_row " + std::to_string(t.lanes_per_row) +
+                                          ", rows_per_wg " + std::to_string(t.rows_per_wg) + ", threads " +
+                                          std::to_string(t.threads) + ", unroll " + std::to_string(t.unroll) +
+                                          ") does not fit M=" + std::to_string(M) + " N=" + std::to_string(N) +
+                                          " K=" + std::to_string(K) + "; smk_set_gemv_tuning(0, 0, 0, 0) restores "
+                                          "the built-in choice");
+    return hip_fail(e, "gemv launch");
+}
+
+int check_gemv_args(int M, int N, int K, const void* x, const void* W, const void* y) {
+    if (M < 0 || N < 0 || K < 0) return fail(SMK_ERR_ARGUMENT, "M, N and K must be >= 0");
+    if (K % 32) return fail(SMK_ERR_ARGUMENT, "K must be a multiple of 32");
+    if (M > 0 && N > 0 && (!y || (K > 0 && (!x || !W)))) return fail(SMK_ERR_ARGUMENT, "null pointer");
+    return SMK_OK;
+}
+
 }  // namespace smk::abi
 
 namespace {
@@ -242,39 +275,6 @@ int download(Ctx* c, void* dst, const void* src, size_t n) {
     return SMK_OK;
 }
 
-// Diagnostics settings of the quantized GEMV (smk_set_*): written under g_tuning_mu, read as a
-// snapshot by every launch, so a setter running beside calls in flight never tears a read.
-std::mutex g_tuning_mu;
-smk::GemvTuning g_tuning;
-
-smk::GemvTuning tuning_now() {
-    std::lock_guard<std::mutex> lk(g_tuning_mu);
-    return g_tuning;
-}
-
-bool tuning_forced(const smk::GemvTuning& t) { return t.lanes_per_row || t.rows_per_wg || t.threads || t.unroll; }
-
-// A launch refused under forced diagnostics settings: the settings do not fit this shape (LDS,
-// lanes, rows) -- say so rather than report a bare launch error.  Out-of-memory keeps its code.
-int gemv_launch_fail(hipError_t e, const smk::GemvTuning& t, int M, int N, int K) {
-    if (e != hipErrorOutOfMemory && e != hipErrorMemoryAllocation && tuning_forced(t))
-        return fail(SMK_ERR_ARGUMENT, std::string("gemv launch (") + hipGetErrorString(e) +
-                                          "): the forced tuning (lanes_per_row " + std::to_string(t.lanes_per_row) +
-                                          ", rows_per_wg " + std::to_string(t.rows_per_wg) + ", threads " +
-                                          std::to_string(t.threads) + ", unroll " + std::to_string(t.unroll) +
-                                          ") does not fit M=" + std::to_string(M) + " N=" + std::to_string(N) +
-                                          " K=" + std::to_string(K) + "; smk_set_gemv_tuning(0, 0, 0, 0) restores "
-                                          "the built-in choice");
-    return hip_fail(e, "gemv launch");
-}
-
-int check_gemv_args(int M, int N, int K, const void* x, const void* W, const void* y) {
-    if (M < 0 || N < 0 || K < 0) return fail(SMK_ERR_ARGUMENT, "M, N and K must be >= 0");
-    if (K % 32) return fail(SMK_ERR_ARGUMENT, "K must be a multiple of 32");
-    if (M > 0 && N > 0 && (!y || (K > 0 && (!x || !W)))) return fail(SMK_ERR_ARGUMENT, "null pointer");
-    return SMK_OK;
-}
-
 // Host-pointer quantized GEMV/GEMM: rows m < M of X [M, K] against W [N, K/32 blocks].
 int host_gemm_quant(int bb, int M, int N, int K, const float* X, const uint8_t* Wq, float* Y) {
     if (const int rc = check_gemv_args(M, N, K, X, Wq, Y)) return rc;
@@ -288,7 +288,7 @@ int host_gemm_quant(int bb, int M, int N, int K, const float* X, const uint8_t* 
     CacheUse use(g_cache_rw);
     const void* wd;
     if (const int rc = weights_on_device(c, Wq, static_cast<size_t>(N) * (K / 32) * bb, &wd)) return rc;
-    const smk::GemvTuning tuning = tuning_now();
+    const smk::GemvTuning tuning = tuning_snapshot();
     // Rows of X in uploads of at most 32 (one matrix-core launch at K <= 4096).
     for (int m0 = 0; m0 < M; m0 += 32) {
         const int mr = std::min(32, M - m0);
@@ -535,7 +535,7 @@ static int d_gemm_quant(int bb, int M, int N, int K, const float* X, int ldx, co
     if (reinterpret_cast<uintptr_t>(X) % 4 || reinterpret_cast<uintptr_t>(Wq) % 2 || reinterpret_cast<uintptr_t>(Y) % 4)
         return fail(SMK_ERR_ARGUMENT, "X and Y must be 4-byte aligned and Wq 2-byte aligned");
     if (const int rc = use_device()) return rc;
-    const smk::GemvTuning tuning = tuning_now();
+    const smk::GemvTuning tuning = tuning_snapshot();
     if (const hipError_t e = smk::gemv_quant(bb, M, N, K, X, ldx, Wq, Y, ldy, S(stream), &tuning); e != hipSuccess)
         return gemv_launch_fail(e, tuning, M, N, K);
     return ok();

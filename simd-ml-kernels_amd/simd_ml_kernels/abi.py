@@ -59,6 +59,7 @@ SIGNATURES = {
     "smk_d_gemv_q4_0": [_i, _i, _p, _p, _p, _p],
     "smk_d_gemv_q8_0": [_i, _i, _p, _p, _p, _p],
     "smk_d_gemm_q4_0": [_i, _i, _i, _p, _i, _p, _p, _i, _p],
+    "smk_d_gemm_q4_0_noalloc": [_i, _i, _i, _p, _i, _p, _p, _i, _p],
     "smk_d_gemm_q8_0": [_i, _i, _i, _p, _i, _p, _p, _i, _p],
     "smk_d_gemm_tb": [_i, _i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i, _p],
     "smk_d_sgemm": [_i, _i, _i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i, _p],
