@@ -51,7 +51,7 @@ int smk_device_info(char* name, size_t name_len, char* arch, size_t arch_len, in
 /* KernelTable::gemv_q4_0, GemvQ4_0Fn (kernels.hpp:52-53, q4_0.hpp:63-72):
  * y[n] = sum_k x[k] W[n][k], W as N*(K/32) GGUF Q4_0 blocks of 18 bytes, K % 32 == 0. */
 int smk_gemv_q4_0(int N, int K, const float* x, const uint8_t* Wq, float* y);
-/* KernelTable::gemv_q8_0, GemvQ8_0Fn (kernels.hpp:50-51, q8_0.hpp:171-178): 34-byte Q8_0 blocks. */
+/* KernelTable::gemv_q8_0, GemvQ8_0Fn (kernels.hpp:50-51, q8_0.hpp:18-28, 93-95): 34-byte Q8_0 blocks. */
 int smk_gemv_q8_0(int N, int K, const float* x, const uint8_t* Wq, float* y);
 /* KernelTable::sgemm, SgemmFn (kernels.hpp:38-41): C = alpha op(A) op(B) + beta C, FP32. */
 int smk_sgemm(int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A, int lda, const float* B,
@@ -69,7 +69,7 @@ int smk_silu(const float* in, float* out, int n);
 int smk_softmax(const float* in, float* out, int rows, int n);
 /* quantize_q4_0_rows (q4_0.hpp:54-60): W [N, K] -> GGUF Q4_0 blocks; SMK_ERR_DATA on rejection. */
 int smk_quantize_q4_0(const float* W, int N, int K, uint8_t* out);
-/* quantize_q8_0_rows (q8_0.hpp:136-142): W [N, K] -> GGUF Q8_0 blocks; SMK_ERR_DATA on rejection. */
+/* quantize_q8_0_rows (q8_0.hpp:53-59): W [N, K] -> GGUF Q8_0 blocks; SMK_ERR_DATA on rejection. */
 int smk_quantize_q8_0(const float* W, int N, int K, uint8_t* out);
 
 /* No reference counterpart (the reference computes these in numpy, examples/llama/llama.py:184-187

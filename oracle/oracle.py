@@ -148,7 +148,7 @@ def _rows_k(W: np.ndarray) -> tuple[np.ndarray, int, int]:
 
 
 def quantize_q4_0(W: np.ndarray) -> np.ndarray:
-    """quantize_q4_0_rows (q4_0_scalar.cpp:468-482) -> uint8 [..., K/32*18]; ValueError on rejection."""
+    """quantize_q4_0_rows (q4_0_scalar.cpp:64-78) -> uint8 [..., K/32*18]; ValueError on rejection."""
     W, rows, K = _rows_k(W)
     out = np.zeros(W.shape[:-1] + (K // 32 * 18,), np.uint8)
     if not lib().smko_quantize_q4_0_rows(_p(W, _f32p), rows, K, _p(out, _u8p)):
@@ -157,7 +157,7 @@ def quantize_q4_0(W: np.ndarray) -> np.ndarray:
 
 
 def quantize_q8_0(W: np.ndarray) -> np.ndarray:
-    """quantize_q8_0_rows (q8_0_scalar.cpp:291-306) -> uint8 [..., K/32*34]; ValueError on rejection."""
+    """quantize_q8_0_rows (q8_0_scalar.cpp:96-111) -> uint8 [..., K/32*34]; ValueError on rejection."""
     W, rows, K = _rows_k(W)
     out = np.zeros(W.shape[:-1] + (K // 32 * 34,), np.uint8)
     if not lib().smko_quantize_q8_0_rows(_p(W, _f32p), rows, K, _p(out, _u8p)):
@@ -166,7 +166,7 @@ def quantize_q8_0(W: np.ndarray) -> np.ndarray:
 
 
 def quantize_x_q8(x: np.ndarray) -> tuple[np.ndarray, np.ndarray] | None:
-    """quantize_x_q8 (q8_0_scalar.cpp:308-313): int8 quants [K] and FP32 scales [K/32]; None if x is not finite."""
+    """quantize_x_q8 (q8_0_scalar.cpp:113-118): int8 quants [K] and FP32 scales [K/32]; None if x is not finite."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     K = x.shape[0]
     qs = np.zeros(K, np.int8)
@@ -177,7 +177,7 @@ def quantize_x_q8(x: np.ndarray) -> tuple[np.ndarray, np.ndarray] | None:
 
 
 def gemv_q4_0(x: np.ndarray, Wq: np.ndarray, N: int, K: int) -> np.ndarray:
-    """Scalar-table gemv_q4_0 semantics (q4_0_scalar.cpp:486-509 under q8_0_scalar.cpp:315-361)."""
+    """Scalar-table gemv_q4_0 semantics (q4_0_scalar.cpp:82-105 under q8_0_scalar.cpp:120-166)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     Wq = np.ascontiguousarray(Wq, dtype=np.uint8)
     y = np.zeros(N, np.float32)
@@ -186,7 +186,7 @@ def gemv_q4_0(x: np.ndarray, Wq: np.ndarray, N: int, K: int) -> np.ndarray:
 
 
 def gemv_q8_0(x: np.ndarray, Wq: np.ndarray, N: int, K: int) -> np.ndarray:
-    """Scalar-table gemv_q8_0 semantics (q8_0_scalar.cpp:365-387)."""
+    """Scalar-table gemv_q8_0 semantics (q8_0_scalar.cpp:170-192)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     Wq = np.ascontiguousarray(Wq, dtype=np.uint8)
     y = np.zeros(N, np.float32)
@@ -265,7 +265,7 @@ def silu_simd(x: np.ndarray) -> np.ndarray:
 
 
 def softmax_simd(x: np.ndarray) -> np.ndarray:
-    """Rows of x through softmax_row_avx2's order (softmax_avx2.cpp:94-186)."""
+    """Rows of x through softmax_row_avx2's order (softmax_avx2.cpp:95-186)."""
     x = np.ascontiguousarray(x, np.float32)
     y = np.empty_like(x)
     n = x.shape[-1]
@@ -342,7 +342,7 @@ def q4_0_split(Wq: np.ndarray, n: int, k: int) -> tuple[np.ndarray, np.ndarray]:
 
 
 def x_scales(x: np.ndarray) -> np.ndarray:
-    """FP32 dx = max|x|/127 per block (q8_0.hpp:103-105)."""
+    """FP32 dx = max|x|/127 per block (q8_0.hpp:20-22)."""
     amax = np.abs(np.asarray(x, np.float32)).reshape(-1, 32).max(axis=1)
     return (amax / np.float32(127)).astype(np.float32)
 

@@ -33,7 +33,7 @@ static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 
 /* binary32 -> binary16, round to nearest even; NaN -> 0x7e00 with the sign,
- * |f| >= 65520 -> infinity.  Semantics of q8_0_scalar.cpp:260-276. */
+ * |f| >= 65520 -> infinity.  Semantics of q8_0_scalar.cpp:65-81. */
 uint16_t smko_fp32_to_fp16(float f) {
     const uint32_t u = f2u(f);
     const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
@@ -53,7 +53,7 @@ uint16_t smko_fp32_to_fp16(float f) {
     return sign | (uint16_t)h;
 }
 
-/* binary16 -> binary32, exact (q8_0_scalar.cpp:278-289). */
+/* binary16 -> binary32, exact (q8_0_scalar.cpp:83-94). */
 float smko_fp16_to_fp32(uint16_t h) {
     const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
     const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
@@ -72,7 +72,7 @@ static void store_scale(uint8_t* out, uint16_t h) {
     out[1] = (uint8_t)(h >> 8);
 }
 
-/* One Q8_0 block (ggml quantize_row_q8_0_ref; q8_0_scalar.cpp:237-256):
+/* One Q8_0 block (ggml quantize_row_q8_0_ref; q8_0_scalar.cpp:36-61):
  * d = amax/127, q = roundf(w * (1/d)) half away from zero, q = 0 when 1/d overflows. */
 static int q8_block(const float* w, int8_t* q, float* d_out) {
     float amax = 0.0f;
@@ -110,7 +110,7 @@ int smko_quantize_x_q8(const float* x, int K, int8_t* qs, float* dx) {
     return 1;
 }
 
-/* One Q4_0 block (ggml quantize_row_q4_0_ref; q4_0_scalar.cpp:427-464): max = the first
+/* One Q4_0 block (ggml quantize_row_q4_0_ref; q4_0_scalar.cpp:23-60): max = the first
  * value of largest magnitude, d = max / -8, q = min(15, trunc(w*id + 8.5)) with the
  * product and the sum rounded separately, id = 0 when d = 0 or 1/d overflows. */
 static int q4_block(const float* w, uint8_t* qs, float* d_out) {
@@ -181,9 +181,9 @@ void smko_block_sums_q4_0(int N, int K, const int8_t* qs, const uint8_t* Wq, int
             out[(size_t)n * nb + b] = q4_isum(Wq + ((size_t)n * nb + b) * 18, qs + 32 * b);
 }
 
-/* The driver's rules (q8_0_scalar.cpp:315-361): N <= 0 writes nothing, K <= 0 gives
+/* The driver's rules (q8_0_scalar.cpp:120-166): N <= 0 writes nothing, K <= 0 gives
  * zeros, a non-finite x gives NaN everywhere; blocks summed in order, one rounding per
- * step: acc += float(isum) * (dw * dx) (q8_0_scalar.cpp:365-381, q4_0_scalar.cpp:486-503). */
+ * step: acc += float(isum) * (dw * dx) (q8_0_scalar.cpp:170-186, q4_0_scalar.cpp:82-99). */
 static void gemv_blocks(int N, int K, const float* x, const uint8_t* Wq, float* y, int q4) {
     if (N <= 0) return;
     if (K <= 0) { for (int n = 0; n < N; ++n) y[n] = 0.0f; return; }
@@ -393,7 +393,7 @@ void smko_silu_simd(const float* in, float* out, int n) {
     }
 }
 
-/* softmax_row_avx2 (softmax_avx2.cpp:94-186): NaN rows as the scalar kernel; then per full
+/* softmax_row_avx2 (softmax_avx2.cpp:95-186): NaN rows as the scalar kernel; then per full
  * group of 8 e = fast_exp(x - max) stored as float, its double added to eight running double
  * sums (lane j of the group into sum j); those eight are added in order (s0+s1+...+s7) to 0;
  * the last n % 8 values use e = exp(double(x - max)) (glibc) added in order; every output is

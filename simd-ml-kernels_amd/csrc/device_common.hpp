@@ -133,9 +133,9 @@ __device__ __forceinline__ int round_half_away(float v) {
 }
 
 // Q8 quants of one quad of x (values 4k..4k+3 of a 32-value block whose 8 quads sit in 8
-// consecutive lanes, which call this together): quantize_row_q8_0 (q8_0_scalar.cpp:237-256)
+// consecutive lanes, which call this together): quantize_row_q8_0 (q8_0_scalar.cpp:36-61)
 // -- d = amax / 127 (IEEE division), id = 1 / d (0 when d is 0 or 1/d overflows float,
-// q8_0_scalar.cpp:249-252), q = round half away from zero (v * id), every product rounded on
+// q8_0_scalar.cpp:33-40, 52-58), q = round half away from zero (v * id), every product rounded on
 // its own.  fin = 0 when one of the quad's values is a NaN or an infinity; such a quad keeps
 // q = 0.  Returns the four quants as bytes of one dword, value 4k in the low byte.
 __device__ __forceinline__ uint32_t q8_quad(const float (&v)[4], float& d, int (&q)[4], int& fin) {

@@ -4,7 +4,7 @@
 // simd_math.hpp:63-117): x / (1 + exp(-x)), IEEE division, the denominator forced to +inf
 // when -x > 88 (so SiLU(-inf) is NaN and very negative x give -0).
 //
-// Softmax rows follow softmax_row_avx2 (softmax_avx2.cpp:94-186): a NaN or +inf anywhere, or
+// Softmax rows follow softmax_row_avx2 (softmax_avx2.cpp:95-186): a NaN or +inf anywhere, or
 // every entry -inf, gives a NaN row; values of full groups of 8 get e = exp(x - max) by the
 // same exp, and their doubles go to eight running double sums (element i into sum i % 8, in
 // order), added as s0 + s1 + ... + s7; the last n % 8 values use a double exp of (x - max)

@@ -1,7 +1,7 @@
 // gemv_quant.hip -- decode GEMV y = x * W^T on GGUF Q4_0 / Q8_0 blocks, for gfx950.
 //
 // Semantics are those of the reference's gemv_q4_0 / gemv_q8_0 (q4_0.hpp:23-33,
-// q8_0.hpp:101-112, driver q8_0_scalar.cpp:315-361): x is quantized once to Q8 blocks
+// q8_0.hpp:18-28, driver q8_0_scalar.cpp:120-166): x is quantized once to Q8 blocks
 // (int8 quants, FP32 scales dx = amax/127), every 32-term block product is an exact
 // int32, and y[n] = sum_b fp16(dw[n][b]) * dx[b] * isum[n][b] in FP32.
 //
@@ -14,7 +14,7 @@
 //
 // Per workgroup (256 threads = 4 waves):
 //   1. issue the first pair loads of W (so HBM latency overlaps step 2),
-//   2. quantize x into LDS, bit-exact with quantize_x_q8 (q8_0_scalar.cpp:237-256,
+//   2. quantize x into LDS, bit-exact with quantize_x_q8 (q8_0_scalar.cpp:36-61,
 //      308-313): IEEE amax/127 and 1/d, product and rounding as separate operations,
 //      ties away from zero.  Q4_0 also stores -8 * sum(qx) per block, the starting
 //      value of the block's dot so that sum((q-8)*qx) = sum(q*qx) - 8*sum(qx)

@@ -1,9 +1,9 @@
 // quantize.hip -- GGUF Q4_0 / Q8_0 weight quantization on the device, and the HBM read roof.
 //
 // Bit-exact with ggml's reference quantizers as the reference restates them:
-//   Q8_0 (q8_0_scalar.cpp:237-306): amax = max|w|, d = amax/127, id = 1/d (0 if d = 0 or
+//   Q8_0 (q8_0_scalar.cpp:36-111): amax = max|w|, d = amax/127, id = 1/d (0 if d = 0 or
 //     1/d overflows), q = roundf(w*id) half away from zero, scale = fp16(d).
-//   Q4_0 (q4_0_scalar.cpp:427-482): max = the FIRST value of largest magnitude, d = max/-8,
+//   Q4_0 (q4_0_scalar.cpp:23-78): max = the FIRST value of largest magnitude, d = max/-8,
 //     id as above, q = min(15, trunc(w*id + 8.5)) with the product and the sum rounded
 //     separately (this file is built with -ffp-contract=off), byte j = q[j] | q[16+j] << 4.
 // A block with a NaN/Inf, or whose scale rounds to fp16 infinity, sets *bad.

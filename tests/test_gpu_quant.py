@@ -1,6 +1,6 @@
 """GPU parity of the quantized decode path against the CPU oracle (oracle/), through the C ABI.
 
-Bars (the reference's own, q4_0.hpp:25-30, q8_0.hpp:103-109):
+Bars (the reference's own, q4_0.hpp:25-30, q8_0.hpp:18-28):
   * x's Q8 quants and FP32 scales: bit-exact;
   * every per-block int32 sum: bit-exact;
   * weight quantizers: byte-exact (llama.cpp fixture, special blocks, random);
