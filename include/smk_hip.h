@@ -121,6 +121,12 @@ int smk_d_quantize(int block_bytes, long long rows, int K, const float* W, uint8
 /* Parity helpers: x's Q8 quants/scales (bad as above) and per-block int32 sums [N, K/32]. */
 int smk_d_quantize_x_q8(int K, const float* x, int8_t* qs, float* dx, int* bad, void* stream);
 int smk_d_block_sums(int block_bytes, int N, int K, const int8_t* qs, const uint8_t* Wq, int32_t* out, void* stream);
+/* Self-check of the x quantizer (no reference counterpart): the device's division-free forms of
+ * d = amax / 127, id = 1 / d (q8_0_scalar.cpp:52-57) and roundf (:33-40) against IEEE division
+ * and the trunc / remainder rounding, over every finite amax >= 0 and every |p| <= 127.5 (about
+ * 4.3e9 cases, one synchronous call).  mismatches[0]: scale cases that differ, mismatches[1]:
+ * rounding cases that differ; both 0 on a correct device. */
+int smk_selfcheck_q8(unsigned* mismatches);
 /* HBM read roof: streams nbytes from src (16-byte aligned) with plain or non-temporal 16-byte
  * loads; sink: >= 2048 floats, never read back. */
 int smk_d_read_roof(const void* src, size_t nbytes, float* sink, int nontemporal, void* stream);

@@ -125,11 +125,28 @@ __device__ __forceinline__ uint32_t skip2(uint32_t hi, uint32_t lo) {
     return __builtin_amdgcn_alignbyte(hi, lo, 2);
 }
 
-// roundf for |v| <= 127.5: half away from zero (v - trunc(v) is exact).
+// roundf for |v| <= 127.5: half away from zero.  v + copysign(0.5 - 2^-25, v) rounds to a value
+// whose truncation is roundf(v) for every float of that range (checked exhaustively on the CPU
+// against the trunc / remainder form: the sum rounds up exactly when |v| has a fraction >= 1/2),
+// so it is one add, one bit select and one truncating conversion.
 __device__ __forceinline__ int round_half_away(float v) {
-    const float t = truncf(v);
-    const float r = v - t;
-    return static_cast<int>(t) + (r >= 0.5f ? 1 : 0) - (r <= -0.5f ? 1 : 0);
+    return static_cast<int>(v + copysignf(0.49999997f, v));
+}
+
+// The block scale of the Q8 quantizers and its inverse, as the reference rounds them (IEEE
+// divisions, q8_0_scalar.cpp:52-57): d = amax / 127, id = 1 / d, id = 0 when d is 0 or 1/d
+// overflows.  Division-free forms with the same results for every finite amax >= 0 (all 2^31 of
+// them checked on gfx950): d is the product by RN(1/127) corrected once by a fused residual; id
+// is v_rcp_f32 refined by one fused Newton step, except for a subnormal d (which v_rcp_f32
+// flushes), where the division is kept.
+__device__ __forceinline__ void q8_scale(float amax, float& d, float& id) {
+    constexpr float c = 1.0f / 127.0f;
+    const float q0 = amax * c;
+    d = fmaf(fmaf(-q0, 127.0f, amax), c, q0);
+    float r = __builtin_amdgcn_rcpf(d);
+    r = fmaf(fmaf(-d, r, 1.0f), r, r);
+    if (d < 1.17549435e-38f) r = d != 0.0f ? 1.0f / d : 0.0f;
+    id = r <= 3.40282347e38f ? r : 0.0f;
 }
 
 // Q8 quants of one quad of x (values 4k..4k+3 of a 32-value block whose 8 quads sit in 8
@@ -142,9 +159,8 @@ __device__ __forceinline__ uint32_t q8_quad(const float (&v)[4], float& d, int (
     fin = finite_bits(v[0]) & finite_bits(v[1]) & finite_bits(v[2]) & finite_bits(v[3]);
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     amax = group_max<8>(amax);
-    d = amax / 127.0f;
-    float id = d != 0.0f ? 1.0f / d : 0.0f;
-    if (!(id <= 3.40282347e38f)) id = 0.0f;
+    float id;
+    q8_scale(amax, d, id);
 #pragma unroll
     for (int i = 0; i < 4; ++i) q[i] = fin ? round_half_away(v[i] * id) : 0;
     return (static_cast<uint32_t>(q[0]) & 0xffu) | ((static_cast<uint32_t>(q[1]) & 0xffu) << 8) |
@@ -163,9 +179,8 @@ __device__ __forceinline__ void q8_oct(const float (&va)[4], const float (&vb)[4
     float amax = fmaxf(fmaxf(fmaxf(fabsf(va[0]), fabsf(va[1])), fmaxf(fabsf(va[2]), fabsf(va[3]))),
                        fmaxf(fmaxf(fabsf(vb[0]), fabsf(vb[1])), fmaxf(fabsf(vb[2]), fabsf(vb[3]))));
     amax = group_max<4>(amax);
-    d = amax / 127.0f;
-    float id = d != 0.0f ? 1.0f / d : 0.0f;
-    if (!(id <= 3.40282347e38f)) id = 0.0f;
+    float id;
+    q8_scale(amax, d, id);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         qa[i] = fa ? round_half_away(va[i] * id) : 0;

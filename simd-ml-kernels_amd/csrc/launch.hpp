@@ -80,6 +80,11 @@ const char* gemv_quant_path(int block_bytes, int N, int K, const uint8_t* W);
 // holds a NaN or +-Inf.  Bit-exact with the reference's quantize_x_q8.
 hipError_t quantize_x_q8(int K, const float* x, int8_t* qs, float* dx, int* bad, hipStream_t stream);
 
+// Exhaustive device check of the x quantizer's division-free scale and rounding against the IEEE
+// forms: counts[0] += scale mismatches, counts[1] += rounding mismatches (counts zeroed by the
+// caller; 0 and 0 expected).
+hipError_t q8_selfcheck(unsigned* counts, hipStream_t stream);
+
 // Per-block int32 sums of x's Q8 quants against W's blocks: out [N, K/32].
 hipError_t block_sums(int block_bytes, int N, int K, const int8_t* qs, const uint8_t* W, int32_t* out,
                       hipStream_t stream);

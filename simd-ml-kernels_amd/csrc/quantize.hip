@@ -177,7 +177,42 @@ __global__ __launch_bounds__(256) void copy_kernel(u32x4* __restrict__ dst, cons
         for (int t = 0; t < tail; ++t) tail_dst[t] = tail_src[t];
 }
 
+// Exhaustive check of the x quantizer's division-free forms (q8_scale, round_half_away) against
+// the IEEE forms they stand for: every finite amax >= 0 (bit patterns below 0x7f800000) through
+// d = amax / 127 and id = 1 / d, and every float p with |p| <= 127.5 through roundf's trunc /
+// remainder form.  counts[0] += scale mismatches, counts[1] += rounding mismatches (one
+// vector atomic per thread that found any).
+__global__ __launch_bounds__(256) void q8_selfcheck_kernel(unsigned* counts) {
+    const uint32_t stride = gridDim.x * blockDim.x;
+    unsigned bad_scale = 0, bad_round = 0;
+    for (uint32_t u = blockIdx.x * blockDim.x + threadIdx.x; u < 0x7f800000u; u += stride) {
+        const float amax = __uint_as_float(u);
+        float d, id;
+        q8_scale(amax, d, id);
+        const float d_ref = amax / 127.0f;
+        float id_ref = d_ref != 0.0f ? 1.0f / d_ref : 0.0f;
+        if (!(id_ref <= 3.40282347e38f)) id_ref = 0.0f;
+        bad_scale += (__float_as_uint(d) != __float_as_uint(d_ref)) | (__float_as_uint(id) != __float_as_uint(id_ref));
+        if (u <= 0x42ff0000u) {  // |p| <= 127.5, both signs
+#pragma unroll
+            for (int sign = 0; sign < 2; ++sign) {
+                const float p = __uint_as_float(u | (sign ? 0x80000000u : 0u));
+                const float t = truncf(p), r = p - t;
+                const int want = static_cast<int>(t) + (r >= 0.5f ? 1 : 0) - (r <= -0.5f ? 1 : 0);
+                bad_round += round_half_away(p) != want;
+            }
+        }
+    }
+    if (bad_scale) atomicAdd(&counts[0], bad_scale);
+    if (bad_round) atomicAdd(&counts[1], bad_round);
+}
+
 }  // namespace
+
+hipError_t q8_selfcheck(unsigned* counts, hipStream_t s) {
+    hipLaunchKernelGGL(q8_selfcheck_kernel, dim3(4096), dim3(256), 0, s, counts);
+    return hipGetLastError();
+}
 
 hipError_t copy_bytes(void* dst, const void* src, size_t bytes, hipStream_t s) {
     if (bytes == 0) return hipSuccess;

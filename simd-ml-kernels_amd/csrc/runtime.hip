@@ -614,6 +614,19 @@ int smk_d_quantize_x_q8(int K, const float* x, int8_t* qs, float* dx, int* bad, 
     return ok();
 }
 
+int smk_selfcheck_q8(unsigned* mismatches) {
+    if (!mismatches) return fail(SMK_ERR_ARGUMENT, "null pointer");
+    if (const int rc = use_device()) return rc;
+    unsigned* d = nullptr;
+    SMK_HIP(hipMalloc(&d, 2 * sizeof(unsigned)), "hipMalloc");
+    hipError_t e = hipMemset(d, 0, 2 * sizeof(unsigned));
+    if (e == hipSuccess) e = smk::q8_selfcheck(d, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(mismatches, d, 2 * sizeof(unsigned), hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    SMK_HIP(e, "q8 self-check");
+    return ok();
+}
+
 int smk_d_block_sums(int bb, int N, int K, const int8_t* qs, const uint8_t* Wq, int32_t* out, void* stream) {
     if ((bb != smk::kQ4_0Bytes && bb != smk::kQ8_0Bytes) || N < 0 || K < 0 || K % 32)
         return fail(SMK_ERR_ARGUMENT, "block_bytes 18 or 34, N >= 0, K % 32 == 0 required");

@@ -70,6 +70,7 @@ SIGNATURES = {
     "smk_d_quantize": [_i, _ll, _i, _p, _p, _p, _p],
     "smk_d_quantize_x_q8": [_i, _p, _p, _p, _p, _p],
     "smk_d_block_sums": [_i, _i, _i, _p, _p, _p, _p],
+    "smk_selfcheck_q8": [_p],
     "smk_d_read_roof": [_p, _sz, _p, _i, _p],
     "smk_d_copy": [_p, _p, _sz, _p],
     "smk_llama_create": [_p, ctypes.POINTER(_p)],

@@ -10,6 +10,7 @@ At the BASELINE shapes (8192x2048, 2048x8192, 14336x4096, 128256x4096) the same 
 checked in full, plus a checksum-of-checksums property on the rotated copies of the bench.
 """
 
+import ctypes
 import os
 
 import numpy as np
@@ -60,6 +61,14 @@ class TestXQuant:
         np.testing.assert_array_equal(g.host(qd, np.int8, K), qs_ref)
         np.testing.assert_array_equal(g.host(dd, np.uint32, K // 32), dx_ref.view(np.uint32))
         assert g.host(bad, np.int32)[0] == 0
+
+    def test_division_free_scale_and_rounding_exhaustive(self):
+        """The quantizer's division-free d = amax/127, id = 1/d and roundf (device_common.hpp
+        q8_scale, round_half_away) equal the IEEE forms for every finite amax >= 0 and every
+        |p| <= 127.5, checked on the device itself (smk_selfcheck_q8)."""
+        out = (ctypes.c_uint * 2)()
+        g.call("smk_selfcheck_q8", ctypes.addressof(out))
+        assert (out[0], out[1]) == (0, 0), f"scale mismatches {out[0]}, rounding mismatches {out[1]}"
 
     def test_nonfinite_flag(self):
         x = np.ones(256, np.float32)
