@@ -52,7 +52,8 @@ def parse():
                         "(M = 1, 2, 4, 8, 32 at 14336x4096, both kernels); decode-eager: only the decode "
                         "model, its 159 positions stepped one kernel at a time with per-section events "
                         "(a profiler-friendly breakdown)")
-    p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
+    p.add_argument("--cpu-seconds", type=float, default=16.0,
+                   help="budget of the CPU baseline's GEMV samples (the decode baseline adds a few seconds)")
     p.add_argument("--no-cpu", action="store_true")
     return p.parse_args()
 
@@ -100,23 +101,62 @@ class Dev:
         return a.elapsed_ms(b) * 1e-3
 
 
+FLUSH_BYTES = 1 << 30
+RAMP_READS = 128  # x 1 GiB: about 20 ms at 7 TB/s
+
+
 def time_launches(dev: Dev, launch, n_copies: int, steps: int, warmup: int, mode: str) -> float:
-    """Average seconds per launch over `steps` launches, HIP events on the launch stream."""
-    for i in range(warmup):
-        launch(i % n_copies)
+    """Average seconds per launch over exactly `steps` launches, HIP events on the launch stream.
+
+    First about 20 ms of HBM reads (clock ramp), `warmup` launches, then (when `steps` launches
+    cannot rotate through all the copies, i.e. fewer than ROTATE_BYTES of distinct weights) a 1 GiB
+    read that evicts the caches, then the `steps` timed launches on copies the warm-up did not
+    touch last, between two events.
+    Graph mode captures the warm-up (with the eviction) and the timed launches as two graphs and
+    records the events around the second one's launch; stream mode issues the launches from
+    Python."""
+    flush = dev.abi.Buffer.filled(FLUSH_BYTES, 5)
+    sink = dev.empty(4 * 4096)
+
+    def warm():
+        # Clock ramp: ~20 ms of HBM reads before the warm-up launches (after an idle host gap
+        # the first milliseconds of work run slower, which a few short launches would not absorb).
+        for _ in range(RAMP_READS):
+            dev.abi.call("smk_d_read_roof", flush.ptr, FLUSH_BYTES, sink.ptr, 0, dev.sp)
+        for i in range(warmup):
+            launch(i % n_copies)
+        if steps < n_copies:  # the timed copies must not be in the caches
+            dev.abi.call("smk_d_read_roof", flush.ptr, FLUSH_BYTES, sink.ptr, 0, dev.sp)
+
+    def timed():
+        for i in range(steps):
+            launch((warmup + i) % n_copies)
+
+    a, b = dev.abi.Event(), dev.abi.Event()
+    launch(0)  # eager first call: a path's scratch (the batched product's) is sized outside any capture
     dev.stream.synchronize()
     if mode == "graph":
-        per_graph = n_copies * max(1, 256 // n_copies) if n_copies < 256 else n_copies
-        with dev.abi.Graph.capture(dev.stream) as cap:
-            for i in range(per_graph):
-                launch(i % n_copies)
-        g = cap.graph
-        reps = max(1, steps // per_graph)
-        g.launch(dev.stream)
+        with dev.abi.Graph.capture(dev.stream) as cap_w:
+            warm()
+        with dev.abi.Graph.capture(dev.stream) as cap_t:
+            timed()
+        gw, gt = cap_w.graph, cap_t.graph
+        gw.launch(dev.stream)  # first replays: code objects and page tables warm
+        gt.launch(dev.stream)
         dev.stream.synchronize()
-        return dev.timed(lambda: g.launch(dev.stream), reps) / (reps * per_graph)
-    it = iter(range(steps))
-    return dev.timed(lambda: launch(next(it) % n_copies), steps) / steps
+        # The warm-up runs right before the timed launches, with no host wait between them: after
+        # an idle gap the first launches run measurably slower (clocks ramp up again).
+        gw.launch(dev.stream)
+        a.record(dev.stream)
+        gt.launch(dev.stream)
+        b.record(dev.stream)
+    else:
+        warm()
+        a.record(dev.stream)
+        timed()
+        b.record(dev.stream)
+    dev.stream.synchronize()
+    return a.elapsed_ms(b) * 1e-3 / steps
 
 
 def quant_case(dev: Dev, fmt: str, N: int, K: int, seed: int, steps: int, warmup: int, mode: str, M: int = 1):
@@ -219,7 +259,7 @@ def copy_roof(dev: Dev, nbytes: int = 256 << 20, reps: int = 5) -> float:
 GOLDEN_TOKENS = os.path.join(ROOT, "tests", "golden", "llama_3_2_1b_q4_0_seed5.json")
 
 
-def decode_case(runs: int = 3) -> dict:
+def decode_case(runs: int = 3, cpu: bool = False) -> dict:
     """the synthetic Llama-3.2-1B (seed 5, Q4_0, written as GGUF by the library's
     own writer and quantizer) through the device decode engine: 32-token prompt, 128 greedy tokens
     (stop_at_eos=False), `runs` times; tok/s = decode steps / decode time (HIP events around the
@@ -258,6 +298,7 @@ def decode_case(runs: int = 3) -> dict:
             wb = m.weight_bytes()
         finally:
             m.close()
+        cpu_dec = cpu_decode_baseline(path, prompt, gold["config"]) if cpu else None
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
     tok_s = float(np.median(tps))
@@ -270,7 +311,8 @@ def decode_case(runs: int = 3) -> dict:
             "tokens_equal_token_by_token_prefill": ids_tok == ids,
             "gemv_weight_bytes_per_token": int(wb),
             "gemv_weight_GBps": round(wb * tok_s / 1e9, 1), "pct_hbm_peak": round(100 * wb * tok_s / PEAK_HBM, 2),
-            "tokens_match_reference_cpu_loop": ids == gold["tokens"], "model_write_s": round(t_write, 1)}
+            "tokens_match_reference_cpu_loop": ids == gold["tokens"], "model_write_s": round(t_write, 1),
+            "cpu_baseline": cpu_dec}
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4_0_8192x2048_hbm_traffic.md")
@@ -289,49 +331,136 @@ def profiled_traffic() -> int | None:
     return None
 
 
-def cpu_baseline(N: int, K: int, budget_s: float) -> dict | None:
-    """The reference's own gemv_q4_0 (widest table this CPU runs, OpenMP on every allowed core)
-    on a bounded sample of the headline workload, weights rotated past the host caches."""
-    from oracle import oracle as o  # the checker/baseline leg only
-    cores = len(os.sched_getaffinity(0))
-    R = o.ref()
-    rng = np.random.default_rng(0)
-    x = rng.standard_normal(K, dtype=np.float32)
-    w = rng.standard_normal((N, K), dtype=np.float32)
-    w *= np.float32(0.02)
-    wq = o.quantize_q4_0(w)
-    del w
-    copies = [wq] + [wq.copy() for _ in range(math.ceil(ROTATE_BYTES / wq.nbytes))]
-    y = np.zeros(N, np.float32)
-    xp, yp = x.ctypes.data_as(o._f32p), y.ctypes.data_as(o._f32p)
-    if R is not None:
-        isa = o.ref_best_isa()
-        R.ref_set_num_threads(cores)
-        run = lambda c: R.ref_gemv_q4_0(o.ISA[isa], N, K, xp, c.ctypes.data_as(o._u8p), yp)
-        kind, path, used = "reference", f"{isa} table, {R.ref_q8_0_path(o.ISA[isa]).decode()} inner loop", cores
-    else:
-        run = lambda c: o.lib().smko_gemv_q4_0(N, K, xp, c.ctypes.data_as(o._u8p), yp)
-        kind, path, used = "port", "oracle C restatement (scalar)", 1
-    for i in range(5):
-        run(copies[i % len(copies)])
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            return next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
+    except (OSError, StopIteration):
+        return ""
+
+
+def _cpu_time(run, n_copies: int, budget_s: float, min_calls: int = 5) -> tuple[float, int]:
+    """Median seconds per call of run(copy index) over about budget_s, after two warm-up calls."""
+    for i in range(2):
+        run(i % n_copies)
     times = []
     t_end = time.perf_counter() + budget_s
     i = 0
-    while time.perf_counter() < t_end or len(times) < 30:
+    while time.perf_counter() < t_end or len(times) < min_calls:
         t = time.perf_counter()
-        run(copies[i % len(copies)])
+        run(i % n_copies)
         times.append(time.perf_counter() - t)
         i += 1
-    med = float(np.median(times))
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            model = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
-    except (OSError, StopIteration):
-        pass
-    return {"value": wq.nbytes / med / 1e9, "unit": "GB/s", "cores": used, "kind": kind,
-            "sample": f"{len(times)} gemv_q4_0 calls 8192x2048 (median {med * 1e6:.1f} us) over "
-                      f"{len(copies)} rotated host copies ({len(copies) * wq.nbytes / 2 ** 20:.0f} MiB); {path}; {model}"}
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline(budget_s: float) -> dict | None:
+    """The reference's own kernels (oracle/_ref: its widest table on this CPU, OpenMP) on bounded
+    samples of the GPU cases: the headline Q4_0 GEMV on all allowed cores (the line's value) and,
+    on one core and on all of them, Q4_0 at 8192x2048 and 14336x4096, Q8_0 at both Llama-3.2-1B
+    FFN orientations, FP16 and BF16 trans_b GEMVs at 4096x4096.  Weights rotate through more than
+    512 MiB of host copies (per case) so the host caches cannot hold them.  Without oracle/_ref
+    (no reference sources where the library was built): the oracle's scalar C restatement of the
+    headline on one core."""
+    from oracle import oracle as o  # the checker/baseline leg only
+    cores = len(os.sched_getaffinity(0))
+    R = o.ref()
+    model = _cpu_model()
+    rng = np.random.default_rng(0)
+    if R is None:
+        N, K = 8192, 2048
+        x = rng.standard_normal(K, dtype=np.float32)
+        w = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+        wq = o.quantize_q4_0(w)
+        y = np.zeros(N, np.float32)
+        run = lambda c: o.lib().smko_gemv_q4_0(N, K, x.ctypes.data_as(o._f32p), wq.ctypes.data_as(o._u8p),
+                                               y.ctypes.data_as(o._f32p))
+        med, n = _cpu_time(run, 1, budget_s)
+        return {"value": wq.nbytes / med / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{n} gemv_q4_0 calls 8192x2048 (median {med * 1e6:.1f} us), oracle C restatement "
+                          f"(scalar), no rotation; {model}"}
+    isa = o.ref_best_isa()
+    path = R.ref_q8_0_path(o.ISA[isa]).decode()
+    share = budget_s / 16  # per (case, thread count); the headline on all cores gets a quarter
+
+    def gemv_case(fmt: str, N: int, K: int, threads: int, secs: float) -> dict:
+        x = rng.standard_normal(K, dtype=np.float32)
+        w = rng.standard_normal((N, K), dtype=np.float32)
+        w *= np.float32(0.02)
+        y = np.zeros(N, np.float32)
+        xp, yp = x.ctypes.data_as(o._f32p), y.ctypes.data_as(o._f32p)
+        if fmt in ("q4_0", "q8_0"):
+            wq = (o.quantize_q4_0 if fmt == "q4_0" else o.quantize_q8_0)(w)
+            fn = R.ref_gemv_q4_0 if fmt == "q4_0" else R.ref_gemv_q8_0
+            run1 = lambda c: fn(o.ISA[isa], N, K, xp, c.ctypes.data_as(o._u8p), yp)
+        else:
+            if fmt == "f16":
+                xb, wq = x.astype(np.float16).view(np.uint16), w.astype(np.float16).view(np.uint16)
+                fn = R.ref_sgemm_f16
+            else:  # bf16 by truncation, as the GPU case
+                xb, wq = (x.view(np.uint32) >> 16).astype(np.uint16), (w.view(np.uint32) >> 16).astype(np.uint16)
+                fn = R.ref_sgemm_bf16
+            run1 = lambda c: fn(o.ISA[isa], 1, 1, N, K, 1.0, xb.ctypes.data, K, c.ctypes.data, K, 0.0, yp, N)
+        del w
+        copies = [wq] + [wq.copy() for _ in range(math.ceil(ROTATE_BYTES / wq.nbytes))]
+        R.ref_set_num_threads(threads)
+        med, n = _cpu_time(lambda i: run1(copies[i]), len(copies), secs)
+        return {"GBps": round(wq.nbytes / med / 1e9, 2), "us": round(med * 1e6, 2), "calls": n,
+                "weight_bytes": int(wq.nbytes), "copies": len(copies)}
+
+    head = gemv_case("q4_0", 8192, 2048, cores, 4 * share)
+    cases = {}
+    for fmt, N, K in (("q4_0", 8192, 2048), ("q4_0", 14336, 4096), ("q8_0", 8192, 2048), ("q8_0", 2048, 8192),
+                      ("f16", 4096, 4096), ("bf16", 4096, 4096)):
+        key = f"{fmt}_{N}x{K}"
+        cases[key] = {"one_core": gemv_case(fmt, N, K, 1, share)}
+        cases[key]["all_cores"] = head if key == "q4_0_8192x2048" else gemv_case(fmt, N, K, cores, share)
+    R.ref_set_num_threads(cores)
+    return {"value": head["GBps"], "unit": "GB/s", "cores": cores, "kind": "reference",
+            "sample": f"{head['calls']} gemv_q4_0 calls 8192x2048 (median {head['us']:.1f} us) over "
+                      f"{head['copies']} rotated host copies ({head['copies'] * head['weight_bytes'] / 2 ** 20:.0f} "
+                      f"MiB); {isa} table, {path} inner loop; {model}",
+            "isa": isa, "q8_0_path": path, "cpu": model, "cases": cases}
+
+
+def cpu_decode_baseline(path: str, prompt: list[int], config: dict, n_steps: int = 24,
+                        n_prompt: int = 8) -> dict | None:
+    """Decode tok/s of the reference's own kernels (oracle/_ref) through the example's loop
+    (oracle/llama_ref.Decoder, "reference" kind: llama.py:414-505 with gemv_q4_0, sgemm, softmax_row
+    and silu from the reference's table) on the same GGUF model as the GPU decode: n_prompt tokens
+    of the prompt, then n_steps timed greedy steps, on all allowed cores and on one."""
+    from oracle import llama_ref as lr  # the checker/baseline leg only
+    from oracle import oracle as o
+    from simd_ml_kernels.gguf import GGUF
+
+    R = o.ref()
+    if R is None:
+        return None
+    cores = len(os.sched_getaffinity(0))
+    cfg = lr.Cfg.from_config(config)
+    g = GGUF(path)
+    W = {"token_embd": g.tensors["token_embd.weight"].data}
+    for i in range(cfg.n_layers):
+        for nm in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"):
+            W[f"{i}.{nm}"] = g.tensors[f"blk.{i}.{nm}.weight"].data
+    out = {}
+    for threads, key in ((cores, "all_cores"), (1, "one_core")):
+        R.ref_set_num_threads(threads)
+        dec = lr.Decoder(cfg, W, lr.Q4_0, "reference")
+        dec.reset(n_prompt + n_steps + 1)
+        logits = None
+        for t in prompt[:n_prompt]:
+            logits = dec.step(t)
+        steps = n_steps if threads > 1 else max(4, n_steps // 4)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            logits = dec.step(int(np.argmax(logits)))
+        dt = time.perf_counter() - t0
+        out[key] = {"tok_s": round(steps / dt, 2), "ms_per_token": round(1e3 * dt / steps, 2), "steps": steps,
+                    "threads": threads}
+    R.ref_set_num_threads(cores)
+    out["loop"] = "oracle/llama_ref.Decoder 'reference' kind (the example's numpy loop on oracle/_ref kernels)"
+    return out
 
 
 def decode_eager() -> dict:
@@ -411,7 +540,7 @@ def main() -> int:
         cases.update(batched_cases(dev, st, wu, args.mode))
     roof = read_roof(dev, nontemporal=1)
     copy = copy_roof(dev)
-    decode = decode_case() if args.cases == "all" else None
+    decode = decode_case(cpu=not args.no_cpu) if args.cases == "all" else None
     sec = head["us"] * 1e-6
     achieved = head["weight_bytes"] / sec
     out = {
@@ -447,7 +576,9 @@ def main() -> int:
         out["decode_tok_s"] = decode["decode_tok_s"]
         out["decode"] = decode
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(8192, 2048, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        if out["cpu_baseline"] is not None and decode is not None:
+            out["cpu_baseline"]["decode"] = decode.pop("cpu_baseline", None)
     print(json.dumps(out))
     return 0
 
