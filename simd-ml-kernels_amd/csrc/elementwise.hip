@@ -127,8 +127,10 @@ constexpr int kMaxLeaves = 256;  // a chunk of 8192 has at most 128 leaves
 
 struct Node { int start, len; };
 
+// Both walks run on one thread; their stacks sit in LDS (an array indexed at run time would be
+// private memory, i.e. scratch).
 __device__ int enumerate_leaves(int n, Node* leaves) {
-    Node stack[32];
+    __shared__ Node stack[32];
     int sp = 0, cnt = 0;
     stack[sp++] = {0, n};
     while (sp > 0) {
@@ -149,8 +151,8 @@ __device__ int enumerate_leaves(int n, Node* leaves) {
 __device__ float combine_leaves(int n, const float* leaf_sum) {
     // Post-order evaluation with an explicit stack of pending nodes and a value stack.
     struct Frame { int start, len, state; };
-    Frame st[32];
-    float vals[32];
+    __shared__ Frame st[32];
+    __shared__ float vals[32];
     int sp = 0, vp = 0, leaf = 0;
     st[sp++] = {0, n, 0};
     while (sp > 0) {

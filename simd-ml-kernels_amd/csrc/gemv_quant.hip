@@ -1201,7 +1201,9 @@ hipError_t launch_pairs_m1(int lpr, int nt, int u, int N, int K, const float* x,
     if (nt == NT_ && u == U_) return launch_pairs_lpr<BB, U_, 1, NT_>(lpr, 1, N, K, x, ldx, W, y, ldy, rpw, acc, s);
     SMK_PAIRS_M1(256, 1) SMK_PAIRS_M1(256, 2) SMK_PAIRS_M1(256, 4)
     SMK_PAIRS_M1(512, 1) SMK_PAIRS_M1(512, 2) SMK_PAIRS_M1(512, 4)
-    SMK_PAIRS_M1(1024, 1) SMK_PAIRS_M1(1024, 2) SMK_PAIRS_M1(1024, 4)
+    SMK_PAIRS_M1(1024, 1) SMK_PAIRS_M1(1024, 2)
+    // Four Q8_0 rows a lane group at 1024 threads would spill (68-byte pairs, 128 registers a lane).
+    if constexpr (BB == kQ4_0Bytes) { SMK_PAIRS_M1(1024, 4) }
 #undef SMK_PAIRS_M1
     return hipErrorInvalidValue;
 }
@@ -1310,7 +1312,6 @@ hipError_t launch_ordered(int M, int N, int K, const float* x, int ldx, const ui
     if (chunks <= 1) return launch_ordered_ch<LPR, MT, NT, 1>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
     if (chunks <= 2) return launch_ordered_ch<LPR, MT, NT, 2>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
     if (chunks <= 4) return launch_ordered_ch<LPR, MT, NT, 4>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
-    if (chunks <= 8) return launch_ordered_ch<LPR, MT, NT, 8>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
     return hipErrorInvalidValue;
 }
 
@@ -1394,7 +1395,9 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
     const int acc = t ? t->accumulate : 0;
     const int pairs = (K >> 5) / 2;
     constexpr size_t kLdsCap = 150 * 1024;
-    const bool generic = !pair_path_ok(K, W) || ordered_lds_bytes(M, K, 256 / 64) > kLdsCap || pairs > 8 * 64;
+    // Rows of more than 4 * 64 pairs (K > 16384) that the tiled kernel does not take go to the
+    // generic kernel: eight pairs a lane would not fit the row-group kernel's registers.
+    const bool generic = !pair_path_ok(K, W) || ordered_lds_bytes(M, K, 256 / 64) > kLdsCap || pairs > 4 * 64;
     NormArgs nrm;
     nrm.stream = t ? t->stream_weights : 0;
     if (t && t->silu_pairs) {
@@ -1438,9 +1441,11 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
     // order), so it is chosen for speed only.
     // Measured on MI355X: one workgroup per compute unit (its groups pipelined through two
     // phase-1 buffers), 32 lanes per row up to 32 pairs a row and 64 beyond, and the fewest
-    // threads (256 to 1024) whose group covers the workgroup's rows.
+    // threads (256 or 512) whose group covers the workgroup's rows, else 512 (1024 threads, 128
+    // registers a lane, spilled in most forms and measured no faster: decode 1,697 tok/s either way,
+    // lm_head 128256x2048 30.8 / 30.7 us).
     int lpr = (t && t->lanes_per_row) ? t->lanes_per_row : (pairs >= 64 ? 64 : pairs >= 16 ? 32 : 16);
-    while (lpr < 64 && (pairs + lpr - 1) / lpr > 8) lpr *= 2;  // at most 8 pairs per lane and row
+    while (lpr < 64 && (pairs + lpr - 1) / lpr > 4) lpr *= 2;  // at most 4 pairs per lane and row
     int rpw = t ? t->rows_per_wg : 0;
     if (rpw <= 0) {
         rpw = std::max(1, (N + g_cus - 1) / g_cus);
@@ -1463,16 +1468,16 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
         int nt = (t && t->threads) ? t->threads : 256;
         const size_t cap = kLdsCap - (nrm.w ? (static_cast<size_t>(K) + (8u << nrm.depth)) * 4 : 0);
         if (!(t && t->threads)) {
-            while (nt < 1024 && nt < rpw * lpr) nt *= 2;
+            while (nt < 512 && nt < rpw * lpr) nt *= 2;
             while (nt > 256 && ordered_lds_bytes(1, K, nt / lpr) > cap) nt /= 2;
         }
         while (ordered_lds_bytes(1, K, nt / lpr) > cap && lpr < (nrm.silu_pairs ? 32 : 64)) lpr *= 2;
         if (nrm.w)  // eight lanes per leaf of the norm's tree, at most four quads of x per thread
             while (nt < (8 << nrm.depth) || nt * 16 < K) nt *= 2;
         switch (nt) {
-            case 1024: return launch_ordered_lpr<1, 1024>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream, nrm);
             case 512: return launch_ordered_lpr<1, 512>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream, nrm);
-            default: return launch_ordered_lpr<1, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream, nrm);
+            case 256: return launch_ordered_lpr<1, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream, nrm);
+            default: return hipErrorInvalidValue;  // 1024 threads: no room for the row groups' registers
         }
     }
     // Several rows of x: 256 threads, 32 or 64 lanes per row (phase 2 needs 4 * rows * M <= 256).

@@ -34,6 +34,18 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_code_objects_have_no_packed_fp32_and_no_scratch():
+    """The built gfx950 code objects (simd-ml-kernels_amd/check_objects.py, also run at link
+    time): no packed-FP32 add/mul/fma instruction and no kernel with a private segment."""
+    build = os.path.join(ROOT, "simd-ml-kernels_amd", "build")
+    if not os.path.isdir(build) or not any(f.endswith(".o") for f in os.listdir(build)):
+        pytest.skip("no build/ objects (the library was built elsewhere)")
+    r = subprocess.run(["python3", os.path.join(ROOT, "simd-ml-kernels_amd", "check_objects.py"), build],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "clean" in r.stdout
+
+
 def test_ctypes_table_matches_header():
     from simd_ml_kernels import abi
     assert sorted(abi.SIGNATURES) == declared()
