@@ -5,8 +5,12 @@
 // every element of B is read once and widened in registers, FP32 fused multiply-adds.
 //
 // Stream kernel (rows 16-byte aligned, K a multiple of 8 elements): LPR lanes share a row of
-// B and each loads 16 bytes per step (8 fp16/bf16 or 4+4 fp32 values); A is staged in LDS as
-// FP32 in K tiles, in two planes of float4 so that lanes read consecutive 16-byte entries.
+// B and each loads 16 bytes per step (8 fp16/bf16 or 4+4 fp32 values).  FP32: A is staged in
+// LDS as FP32 in K tiles, in two planes of float4 so that lanes read consecutive 16-byte
+// entries, and every product is one FMA.  FP16 / BF16: A is staged as it is stored (8 values of
+// 16 bits per 16-byte entry) and each pair of products is one v_dot2_f32_f16 / v_dot2_f32_bf16
+// (exact products: 11- or 8-bit significands; FP32 sums), half the VALU of widening each value
+// first -- which BF16 needs two instructions for (a shift or a mask), FP16 one (v_fma_mix).
 // Everything else (odd K, unaligned rows, M > 8) takes a plain one-thread-per-output kernel.
 #include "device_common.hpp"
 #include "launch.hpp"
@@ -46,6 +50,17 @@ __device__ __forceinline__ void widen(const u32x4& t, float* v) {
     }
 }
 
+// acc + a.lo * b.lo + a.hi * b.hi for two packed FP16 (E = 1) or BF16 (E = 2) values each.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+template <int E>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+    if constexpr (E == 1)
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc, false);
+    else
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), acc, false);
+}
+
 // LPR lanes share a row; a lane takes 8-element groups j, j + LPR, ... of its U rows.  The
 // loads of the next D groups are issued before the current D groups' FMAs (two register
 // buffers), every load unconditional from a clamped row and group so the compiler's wait
@@ -61,7 +76,8 @@ __global__ __launch_bounds__(kThreads) void gemv_lowp_kernel(int M, int N, int K
     constexpr int kRowsPerWg = 4 * G * U;
     constexpr int L = E == 0 ? 2 : 1;             // 16-byte loads per 8-element group
     constexpr size_t kEs = E == 0 ? 4 : 2;
-    extern __shared__ __align__(16) float4 xs[];  // [MT][2][kt/8]
+    extern __shared__ __align__(16) float4 xs[];  // FP32: [MT][2][kt/8] float4; else [MT][kt/8] uint4
+    u32x4* const xh = reinterpret_cast<u32x4*>(xs);
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int g = lane / LPR, j = lane % LPR;
     const int rb = blockIdx.x * kRowsPerWg + wave * G * U + g;
@@ -100,7 +116,33 @@ __global__ __launch_bounds__(kThreads) void gemv_lowp_kernel(int M, int N, int K
         // A tile: 8-element groups, four loaded per thread before any is stored (16-byte loads
         // when A's rows are 16-byte aligned), so its loads wait together once.
         const int ng = M * groups;
-        for (int i0 = threadIdx.x; i0 < ng; i0 += 4 * kThreads) {
+        if constexpr (E != 0) {
+            for (int i0 = threadIdx.x; i0 < ng; i0 += 4 * kThreads) {
+                u32x4 v[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int i = min(i0 + q * kThreads, ng - 1);
+                    const int m = i / groups, grp = i - m * groups;
+                    const size_t base = static_cast<size_t>(m) * lda + k0 + 8 * grp;
+                    if (a_vec) {
+                        v[q] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(A) + base);
+                    } else {
+                        const uint16_t* p = static_cast<const uint16_t*>(A) + base;
+                        v[q] = u32x4{p[0] | (static_cast<uint32_t>(p[1]) << 16), p[2] | (static_cast<uint32_t>(p[3]) << 16),
+                                     p[4] | (static_cast<uint32_t>(p[5]) << 16), p[6] | (static_cast<uint32_t>(p[7]) << 16)};
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int i = i0 + q * kThreads;
+                    if (i < ng) {
+                        const int m = i / groups, grp = i - m * groups;
+                        xh[m * groups_max + grp] = v[q];
+                    }
+                }
+            }
+        }
+        for (int i0 = threadIdx.x; E == 0 && i0 < ng; i0 += 4 * kThreads) {
             float v[4][8];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -135,15 +177,27 @@ __global__ __launch_bounds__(kThreads) void gemv_lowp_kernel(int M, int N, int K
 #pragma unroll
                     for (int m = 0; m < MT; ++m) {
                         if (m >= M) continue;
-                        const float4 xa = xs[(m * 2) * groups_max + c], xb = xs[(m * 2 + 1) * groups_max + c];
-                        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+                        if constexpr (E == 0) {
+                            const float4 xa = xs[(m * 2) * groups_max + c], xb = xs[(m * 2 + 1) * groups_max + c];
+                            const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
-                        for (int u = 0; u < U; ++u) {
-                            float wv[8];
-                            widen<E>(w[d][u][0], wv);
-                            if constexpr (L == 2) widen<E>(w[d][u][1], wv + 4);
+                            for (int u = 0; u < U; ++u) {
+                                float wv[8];
+                                widen<E>(w[d][u][0], wv);
+                                if constexpr (L == 2) widen<E>(w[d][u][1], wv + 4);
 #pragma unroll
-                            for (int e = 0; e < 8; ++e) acc[u][m] = fmaf(xv[e], wv[e], acc[u][m]);
+                                for (int e = 0; e < 8; ++e) acc[u][m] = fmaf(xv[e], wv[e], acc[u][m]);
+                            }
+                        } else {
+                            const u32x4 xq = xh[m * groups_max + c];
+#pragma unroll
+                            for (int u = 0; u < U; ++u) {
+                                const u32x4 wq = w[d][u][0];
+                                acc[u][m] = dot2<E>(xq.x, wq.x, acc[u][m]);
+                                acc[u][m] = dot2<E>(xq.y, wq.y, acc[u][m]);
+                                acc[u][m] = dot2<E>(xq.z, wq.z, acc[u][m]);
+                                acc[u][m] = dot2<E>(xq.w, wq.w, acc[u][m]);
+                            }
                         }
                     }
                 }
