@@ -97,15 +97,17 @@ __global__ void embed_rows_kernel(const uint8_t* __restrict__ E, int type, int h
 //     of 8, eight running double sums, a double exp on the last n % 8);
 //   out = sk.sgemm(p, V): the AVX2 direct product (avx2_gemm_packed.cpp:151-201), one fused
 //     chain over the positions in order per output.
-// One workgroup of 256 threads per query head; scores in LDS; cached K and V read in tiles of
+// One workgroup of kAttnThreads threads per query head; scores in LDS; cached K and V read in tiles of
 // `tile` positions staged through LDS (up to kMaxTile; every position of a decode that fits
 // one tile is read in the first round, together with q, k and v).
-constexpr int kAttnThreads = 256;
+constexpr int kAttnThreads = 512;  // measured: 256 / 512 / 1024 threads, decode 1,694 / 1,715 / 1,675 tok/s
+constexpr int kHeadMax = 256;     // head_dim limit (create() checks it)
+constexpr int kRopeKvThreads = 256;
 constexpr int kMaxTile = 256;
 constexpr size_t kAttnLdsBudget = 150 * 1024;
 
 // count floats (a multiple of 4, 16-byte aligned ends) from global to LDS, four rounds of
-// 256 x 16 bytes (of each source) a batch: every thread issues the batch's loads before storing
+// kAttnThreads x 16 bytes (of each source) a batch: every thread issues the batch's loads before storing
 // any. Every store is unconditional (an element past the end goes to the spare slot `dump`): a
 // load whose only use is a store under a branch is moved by the compiler into that branch, and
 // the rounds then wait for each other one at a time.
@@ -160,7 +162,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
                                                                  float* __restrict__ out, int pos_first,
                                                                  int qkv_stride, int out_stride) {
     extern __shared__ float sc[];  // T scores then probabilities; then the K and V tiles
-    __shared__ float qs[256], ks[256], vs[256];
+    __shared__ float qs[kHeadMax], ks[kHeadMax], vs[kHeadMax];
     __shared__ float red_f[kAttnThreads / kWave];
     __shared__ int red_i[kAttnThreads / kWave];
     __shared__ double lane_sum[8];
@@ -185,16 +187,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     const int first_cached = min(min(tile, T), pos);
     {
         // q, k, v loaded by every thread (a clamped index past head_dim; qs, ks, vs hold
-        // kAttnThreads entries, of which the first hd are read) and stored after the tiles, so
+        // kHeadMax entries, of which the first hd are read) and stored after the tiles, so
         // their loads are not waited for before the tile loads are issued.
         const int d = min(static_cast<int>(threadIdx.x), hd - 1);
         const float q0 = qkv[static_cast<size_t>(head) * hd + d];
         const float k0 = qkv[static_cast<size_t>(n_heads + g) * hd + d];
         const float v0 = qkv[static_cast<size_t>(n_heads + n_kv + g) * hd + d];
         stage_tiles<true>(ktile, K, vtile, V, first_cached * hd, dump);
-        qs[threadIdx.x] = q0;
-        ks[threadIdx.x] = k0;
-        vs[threadIdx.x] = v0;
+        if (threadIdx.x < kHeadMax) {
+            qs[threadIdx.x] = q0;
+            ks[threadIdx.x] = k0;
+            vs[threadIdx.x] = v0;
+        }
     }
     __syncthreads();
     const float* cs = cos_tab + static_cast<size_t>(pos) * hd;
@@ -320,12 +324,12 @@ size_t attention_lds(int cap, int hd) {
 // Prompt chunk: k = rope(k) and v of rows p < gridDim.y into the cache at pos_first + p, for KV
 // group blockIdx.x -- the values attention_kernel writes for a decode step (same operations),
 // so that every row's attention can read the positions before it from the cache.
-__global__ __launch_bounds__(kAttnThreads) void rope_kv_kernel(const float* __restrict__ qkv, int qkv_stride,
+__global__ __launch_bounds__(kRopeKvThreads) void rope_kv_kernel(const float* __restrict__ qkv, int qkv_stride,
                                                                const float* __restrict__ cos_tab,
                                                                const float* __restrict__ sin_tab, int interleaved,
                                                                float* __restrict__ kc, float* __restrict__ vc,
                                                                int n_heads, int n_kv, int hd, int cap, int pos_first) {
-    __shared__ float ks[256];
+    __shared__ float ks[kHeadMax];
     const int g = blockIdx.x, p = blockIdx.y, pos = pos_first + p;
     const float* row = qkv + static_cast<size_t>(p) * qkv_stride;
     const int d = threadIdx.x;
@@ -687,7 +691,7 @@ hipError_t enqueue_prompt_chunk(Model& md, int first, int P, bool with_logits) {
         hipError_t e = rms_norm(md.bx, L.attn_norm, md.bh, P, H, c.rms_eps, s);
         if (e == hipSuccess) e = gemv_quant(bb, P, qkv_rows, H, md.bh, H, L.qkv.p, md.bqkv, qkv_rows, s, &plain);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(rope_kv_kernel, dim3(nkv, P), dim3(kAttnThreads), 0, s, md.bqkv, qkv_rows, md.cos_tab,
+        hipLaunchKernelGGL(rope_kv_kernel, dim3(nkv, P), dim3(kRopeKvThreads), 0, s, md.bqkv, qkv_rows, md.cos_tab,
                            md.sin_tab, c.rope_interleaved, kc, vc, nh, nkv, hd, md.capacity, first);
         hipLaunchKernelGGL(attention_kernel, dim3(nh, P), dim3(kAttnThreads), attention_lds(md.capacity, hd), s,
                            md.bqkv, md.cos_tab, md.sin_tab, c.rope_interleaved, kc, vc, nh, nkv, hd, md.capacity,
