@@ -47,11 +47,15 @@ def parse():
     p.add_argument("--steps", type=int, default=2000, help="timed GEMV launches of the headline case")
     p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--mode", choices=["graph", "stream"], default="graph")
-    p.add_argument("--cases", choices=["all", "headline", "decode", "batched", "decode-eager"], default="all",
+    p.add_argument("--cases", choices=["all", "headline", "decode", "batched", "decode-eager", "shapes"],
+                   default="all",
                    help="decode: only the decode model; batched: only the config 4 Q4_0 products "
                         "(M = 1, 2, 4, 8, 32 at 14336x4096, both kernels); decode-eager: only the decode "
                         "model, its 159 positions stepped one kernel at a time with per-section events "
-                        "(a profiler-friendly breakdown)")
+                        "(a profiler-friendly breakdown); shapes: only the --shape GEMVs")
+    p.add_argument("--shape", action="append", default=None, metavar="FMT:NxK",
+                   help="with --cases shapes: a Q4_0 / Q8_0 / F16 / BF16 GEMV case, e.g. q4_0:14336x4096 "
+                        "(repeatable; default the Llama-3-8B Q4_0 and Q8_0 shapes)")
     p.add_argument("--cpu-seconds", type=float, default=16.0,
                    help="budget of the CPU baseline's GEMV samples (the decode baseline adds a few seconds)")
     p.add_argument("--no-cpu", action="store_true")
@@ -509,6 +513,19 @@ def main() -> int:
         print(json.dumps({"decode": decode_case()}))
         return 0
     dev = Dev()
+    if args.cases == "shapes":
+        out = {}
+        for spec in args.shape or [f"{f}:{n}x{k}" for f in ("q4_0", "q8_0") for n, k in ((14336, 4096), (4096, 14336))]:
+            fmt, dims = spec.split(":")
+            N, K = (int(v) for v in dims.lower().split("x"))
+            if fmt in BB:
+                out[f"{fmt}_{N}x{K}"] = quant_case(dev, fmt, N, K, 3, args.steps, args.warmup, args.mode)
+            elif fmt in ("f16", "bf16"):
+                out[f"{fmt}_{N}x{K}"] = lowp_case(dev, fmt, N, K, 2, args.steps, args.warmup, args.mode)
+            else:
+                raise SystemExit(f"--shape {spec}: format must be one of q4_0, q8_0, f16, bf16")
+        print(json.dumps({"shapes": out}))
+        return 0
     if args.cases == "batched":
         print(json.dumps({"batched": batched_cases(dev, max(200, args.steps // 4), 50, args.mode)}))
         return 0
