@@ -106,33 +106,304 @@ constexpr int kRopeKvThreads = 256;
 constexpr int kMaxTile = 256;
 constexpr size_t kAttnLdsBudget = 150 * 1024;
 
-// count floats (a multiple of 4, 16-byte aligned ends) from global to LDS, four rounds of
-// kAttnThreads x 16 bytes (of each source) a batch: every thread issues the batch's loads before storing
+// Row stride (floats) of the K tile in LDS: one thread reads a whole row for its score, and at
+// this stride the rows of 16 neighbouring lanes start in different banks.
+__host__ __device__ __forceinline__ int k_stride(int hd) { return hd + 4; }
+
+// count floats (a multiple of 4, 16-byte aligned ends) from global to LDS in batches of R rounds
+// of kAttnThreads x 16 bytes (of each source): every thread issues a batch's loads before storing
 // any. Every store is unconditional (an element past the end goes to the spare slot `dump`): a
 // load whose only use is a store under a branch is moved by the compiler into that branch, and
-// the rounds then wait for each other one at a time.
-template <bool kTwo>  // true: d1 from s1 as well
-__device__ __forceinline__ void stage_tiles(float* __restrict__ d0, const float* __restrict__ s0,
-                                            float* __restrict__ d1, const float* __restrict__ s1, int count,
-                                            float* __restrict__ dump) {
+// the rounds then wait for each other one at a time.  d0 takes rows of row4 float4s at a stride
+// of d0_stride floats; d1 is dense.
+template <bool kTwo, int R>  // kTwo: d1 from s1 as well
+__device__ __forceinline__ void stage_rounds(float* __restrict__ d0, const float* __restrict__ s0,
+                                             float* __restrict__ d1, const float* __restrict__ s1, int count,
+                                             float* __restrict__ dump, int row4, int d0_stride) {
     const float4* a4 = reinterpret_cast<const float4*>(s0);
     const float4* b4 = reinterpret_cast<const float4*>(s1);
     const int n4 = count >> 2;
-    for (int base = 0; base < n4; base += 4 * kAttnThreads) {
-        float4 va[4], vb[4];
+    for (int base = 0; base < n4; base += R * kAttnThreads) {
+        float4 va[R], vb[R];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < R; ++u) {
             const int e = base + u * kAttnThreads + static_cast<int>(threadIdx.x);
             va[u] = a4[e < n4 ? e : 0];
             if constexpr (kTwo) vb[u] = b4[e < n4 ? e : 0];
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < R; ++u) {
             const int e = base + u * kAttnThreads + static_cast<int>(threadIdx.x);
-            *reinterpret_cast<float4*>(e < n4 ? d0 + 4 * e : dump) = va[u];
+            const int r = e / row4;
+            *reinterpret_cast<float4*>(e < n4 ? d0 + r * d0_stride + 4 * (e - r * row4) : dump) = va[u];
             if constexpr (kTwo) *reinterpret_cast<float4*>(e < n4 ? d1 + 4 * e : dump) = vb[u];
         }
     }
+}
+// Four rounds a batch, or eight when the data needs more than four (one wait for a whole tile of
+// 256 positions of head_dim 64).
+template <bool kTwo>
+__device__ __forceinline__ void stage_tiles(float* __restrict__ d0, const float* __restrict__ s0,
+                                            float* __restrict__ d1, const float* __restrict__ s1, int count,
+                                            float* __restrict__ dump, int row4, int d0_stride) {
+    if (count > 16 * kAttnThreads)
+        stage_rounds<kTwo, 8>(d0, s0, d1, s1, count, dump, row4, d0_stride);
+    else
+        stage_rounds<kTwo, 4>(d0, s0, d1, s1, count, dump, row4, d0_stride);
+}
+
+// The score of one position, computed by one thread: the reference's 16-lane dot (element e
+// goes to lane e % 16, chain (e / 16) % 2, each chain fused in increasing e from +0), the two
+// chains of a lane added, the 16 lane sums reduced by halves (lanes i and i+8, i and i+4, i and
+// i+2, then the pair), times scale.  q is read from LDS at the same address by every lane; kr is
+// the position's row of the K tile.  HD > 0: head_dim HD; 0: hd at run time.
+template <int HD>
+__device__ __forceinline__ float position_score(const float* __restrict__ qs, const float* __restrict__ kr, int hd,
+                                                float scale) {
+    float a[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) a[i] = 0.0f;
+    const float4* q4 = reinterpret_cast<const float4*>(qs);
+    const float4* k4 = reinterpret_cast<const float4*>(kr);
+    // 32 elements a step (both chains of every lane once); within a step the chain of each
+    // element is a constant.
+    auto step = [&](int p, int n) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (p + 4 * j < n) {
+                const float4 q = q4[p / 4 + j], k = k4[p / 4 + j];
+                const float qv[4] = {q.x, q.y, q.z, q.w}, kv[4] = {k.x, k.y, k.z, k.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int e = 4 * j + i;  // element p + e: lane e % 16, chain e / 16
+                    a[(e >> 4) * 16 + (e & 15)] = fmaf(qv[i], kv[i], a[(e >> 4) * 16 + (e & 15)]);
+                }
+            }
+        }
+    };
+    if constexpr (HD > 0) {
+#pragma unroll
+        for (int p = 0; p < HD; p += 32) step(p, HD);
+    } else {
+        for (int p = 0; p < hd; p += 32) step(p, hd);
+    }
+    float v[16];
+#pragma unroll
+    for (int l = 0; l < 16; ++l) v[l] = a[l] + a[16 + l];
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1) {
+#pragma unroll
+        for (int l = 0; l < w; ++l) v[l] = v[l] + v[l + w];
+    }
+    return scale * v[0];
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __restrict__ qkv,
+                                                                 const float* __restrict__ cos_tab,
+                                                                 const float* __restrict__ sin_tab, int interleaved,
+                                                                 float* __restrict__ kc, float* __restrict__ vc,
+                                                                 int n_heads, int n_kv, int hd_arg, int cap,
+                                                                 float scale, int tile,
+                                                                 const DecodeState* __restrict__ st,
+                                                                 float* __restrict__ out, int pos_first,
+                                                                 int qkv_stride, int out_stride) {
+    constexpr int kWaves = kAttnThreads / kWave;
+    extern __shared__ float sc[];  // T scores then exponentials; then the K and V tiles
+    __shared__ __align__(16) float qs[kHeadMax];
+    __shared__ float ks[kHeadMax], vs[kHeadMax];
+    __shared__ float red_f[kWaves];
+    __shared__ int red_i[kWaves];
+    __shared__ double tail_e[8];
+    __shared__ float inv_s;
+    const int hd = HD > 0 ? HD : hd_arg, kst = k_stride(hd);
+    const int head = blockIdx.x;
+    const int rep = n_heads / n_kv, g = head / rep;
+    // A decode step: the position in DecodeState.  A prompt chunk: row blockIdx.y of qkv / out
+    // at position pos_first + blockIdx.y (every row's k and v already in the cache).
+    const int pos = pos_first >= 0 ? pos_first + static_cast<int>(blockIdx.y) : st->pos, T = pos + 1;
+    qkv += static_cast<size_t>(blockIdx.y) * qkv_stride;
+    out += static_cast<size_t>(blockIdx.y) * out_stride;
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & (kWave - 1), wave = tid / kWave;
+    float* ktile = sc + ((cap + 3) & ~3);   // tile rows of kst floats
+    float* vtile = ktile + tile * kst;      // tile rows of hd floats
+    float* dump = vtile + tile * hd;        // 4 floats: where stores past a tile's end go
+    float* K = kc + static_cast<size_t>(g) * cap * hd;
+    float* V = vc + static_cast<size_t>(g) * cap * hd;
+    const bool one_round = T <= tile;
+
+    // Load phase: this step's q, k, v, the RoPE factors and the first round's cached K and V
+    // (positions < pos), every load issued before any store.  Thread i < hd / 2 rotates pair i
+    // of q and k in registers; thread d < hd carries v[d].  The rotated k and v go to ks / vs,
+    // into the tiles' row pos when the whole context is one round, and (the first workgroup of
+    // the KV group) into the cache.
+    {
+        const int half = hd / 2;
+        const int i = min(tid, half - 1), dv = min(tid, hd - 1);
+        const int ia = interleaved ? 2 * i : i, ib = interleaved ? 2 * i + 1 : half + i;
+        const float* qrow = qkv + static_cast<size_t>(head) * hd;
+        const float* krow = qkv + static_cast<size_t>(n_heads + g) * hd;
+        const float* cs = cos_tab + static_cast<size_t>(pos) * hd;
+        const float* sn = sin_tab + static_cast<size_t>(pos) * hd;
+        const float qa = qrow[ia], qb = qrow[ib], ka = krow[ia], kb = krow[ib];
+        const float c0 = cs[i], s0 = sn[i], c1 = cs[half + i], s1 = sn[half + i];
+        const float v0 = qkv[static_cast<size_t>(n_heads + n_kv + g) * hd + dv];
+        const int first_cached = min(min(tile, T), pos);
+        stage_tiles<true>(ktile, K, vtile, V, first_cached * hd, dump, hd / 4, kst);
+        float q0, q1, k0, k1;
+        if (interleaved) {
+            rope_pair_interleaved(qa, qb, c0, s0, q0, q1);
+            rope_pair_interleaved(ka, kb, c0, s0, k0, k1);
+        } else {
+            rope_pair_half(qa, qb, c0, s0, c1, s1, q0, q1);
+            rope_pair_half(ka, kb, c0, s0, c1, s1, k0, k1);
+        }
+        const bool writer = head % rep == 0;
+        if (tid < half) {
+            qs[ia] = q0;
+            qs[ib] = q1;
+            ks[ia] = k0;
+            ks[ib] = k1;
+            if (one_round) {
+                ktile[pos * kst + ia] = k0;
+                ktile[pos * kst + ib] = k1;
+            }
+            if (writer) {
+                K[static_cast<size_t>(pos) * hd + ia] = k0;
+                K[static_cast<size_t>(pos) * hd + ib] = k1;
+            }
+        }
+        if (tid < hd) {
+            vs[tid] = v0;
+            if (one_round) vtile[pos * hd + tid] = v0;
+            if (writer) V[static_cast<size_t>(pos) * hd + tid] = v0;
+        }
+    }
+    __syncthreads();
+
+    // Scores, `tile` positions a round (one thread a position); rounds after the first restage
+    // the K tile, position pos from ks.
+    for (int t0 = 0; t0 < T; t0 += tile) {
+        const int tn = min(tile, T - t0);
+        if (t0 > 0) {
+            const int cached = min(tn, pos - t0);
+            __syncthreads();  // the previous round's tile is consumed
+            if (cached > 0)
+                stage_tiles<false>(ktile, K + static_cast<size_t>(t0) * hd, nullptr, nullptr, cached * hd, dump,
+                                   hd / 4, kst);
+            if (cached < tn)
+                for (int d = tid; d < hd; d += kAttnThreads) ktile[(pos - t0) * kst + d] = ks[d];
+            __syncthreads();
+        }
+        for (int t = tid; t < tn; t += kAttnThreads) sc[t0 + t] = position_score<HD>(qs, ktile + t * kst, hd, scale);
+    }
+    __syncthreads();
+
+    // Softmax over the T scores: the maximum (and whether any score is NaN or infinite), the
+    // exponentials (the SIMD exp on full groups of 8, double exp on the last T % 8), then the
+    // eight running double sums of the groups of 8 (lane j: positions j, j+8, ... in order),
+    // added in lane order, then the tail's doubles, and 1 / sum.
+    float mx = -__builtin_inff();
+    int nonfinite = 0;
+    for (int t = tid; t < T; t += kAttnThreads) {
+        const float v = sc[t];
+        const uint32_t u = __float_as_uint(v);
+        nonfinite |= (u & 0x7fffffffu) > 0x7f800000u || u == 0x7f800000u;
+        mx = fmaxf(mx, v);
+    }
+    mx = group_max<kWave>(mx);
+    nonfinite = group_sum_int<kWave>(nonfinite);
+    if (lane == 0) {
+        red_f[wave] = mx;
+        red_i[wave] = nonfinite;
+    }
+    __syncthreads();
+    mx = red_f[0];
+    nonfinite = red_i[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+        mx = fmaxf(mx, red_f[w]);
+        nonfinite |= red_i[w];
+    }
+    const bool nan_row = nonfinite || __float_as_uint(mx) == 0xff800000u;
+    const int n8 = T - T % 8;
+    for (int t = tid; t < T; t += kAttnThreads) {
+        const float dd = sc[t] - mx;
+        if (t < n8) {
+            sc[t] = exp_cody_waite(dd);
+        } else {
+            const double e = exp(static_cast<double>(dd));
+            tail_e[t - n8] = e;
+            sc[t] = static_cast<float>(e);
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        double acc = 0.0;
+        if (lane < 8) {
+            int t = lane;
+            for (; t + 56 < n8; t += 64) {  // eight reads issued before the eight adds
+                float e[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) e[u] = sc[t + 8 * u];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc = acc + static_cast<double>(e[u]);
+            }
+            for (; t < n8; t += 8) acc = acc + static_cast<double>(sc[t]);
+        }
+        double tsum = __shfl(acc, 0, kWave);
+#pragma unroll
+        for (int k = 1; k < 8; ++k) tsum = tsum + __shfl(acc, k, kWave);
+        if (lane == 0) {
+            double sum = 0.0 + tsum;
+            for (int t = 0; t < T - n8; ++t) sum = sum + tail_e[t];
+            inv_s = static_cast<float>(1.0 / sum);
+        }
+    }
+    __syncthreads();
+
+    // out[d] = one fused chain over the positions in order of p[t] * V[t][d], p[t] = e[t] / sum
+    // as the product e[t] * (1 / sum) (NaN for a row with a NaN or infinite score).
+    const float inv = nan_row ? __builtin_nanf("") : inv_s;  // NaN * e = NaN for every position
+    float acc = 0.0f;
+    const int d = tid;
+    for (int t0 = 0; t0 < T; t0 += tile) {
+        const int tn = min(tile, T - t0);
+        if (t0 > 0) {
+            const int cached = min(tn, pos - t0);
+            __syncthreads();  // the previous tile is consumed
+            if (cached > 0)
+                stage_tiles<false>(vtile, V + static_cast<size_t>(t0) * hd, nullptr, nullptr, cached * hd, dump,
+                                   hd / 4, hd);
+            if (cached < tn)
+                for (int e = tid; e < hd; e += kAttnThreads) vtile[(pos - t0) * hd + e] = vs[e];
+            __syncthreads();
+        }
+        if (d < hd) {
+#pragma unroll 8
+            for (int t = 0; t < tn; ++t) acc = fmaf(sc[t0 + t] * inv, vtile[t * hd + d], acc);
+        }
+    }
+    if (d < hd) out[static_cast<size_t>(head) * hd + d] = acc;
+}
+
+// Positions per round: the whole cache when it fits kMaxTile, else as many as the LDS budget
+// leaves beside the scores (at least 16).
+int attention_tile(int cap, int hd) {
+    const size_t left = kAttnLdsBudget / 4 - static_cast<size_t>((cap + 3) & ~3) - 4;  // 4: the spare slot
+    const int fit = static_cast<int>(left / static_cast<size_t>(k_stride(hd) + hd));
+    return std::max(16, std::min({kMaxTile, cap, fit}));
+}
+size_t attention_lds(int cap, int hd) {
+    return (static_cast<size_t>((cap + 3) & ~3) + static_cast<size_t>(attention_tile(cap, hd)) * (k_stride(hd) + hd) +
+            4) *
+           4;
+}
+
+// The instantiation for a head_dim: 64 and 128 unrolled, any other the run-time loop.
+using AttentionFn = decltype(&attention_kernel<0>);
+AttentionFn attention_for(int hd) {
+    return hd == 64 ? attention_kernel<64> : hd == 128 ? attention_kernel<128> : attention_kernel<0>;
 }
 
 // RoPE of one head of hd values in place in LDS (hd / 2 threads).
@@ -151,174 +422,6 @@ __device__ __forceinline__ void rope_head_lds(float* v, const float* cs, const f
             v[half + i] = o1;
         }
     }
-}
-
-__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __restrict__ qkv,
-                                                                 const float* __restrict__ cos_tab,
-                                                                 const float* __restrict__ sin_tab, int interleaved,
-                                                                 float* __restrict__ kc, float* __restrict__ vc,
-                                                                 int n_heads, int n_kv, int hd, int cap, float scale,
-                                                                 int tile, const DecodeState* __restrict__ st,
-                                                                 float* __restrict__ out, int pos_first,
-                                                                 int qkv_stride, int out_stride) {
-    extern __shared__ float sc[];  // T scores then probabilities; then the K and V tiles
-    __shared__ float qs[kHeadMax], ks[kHeadMax], vs[kHeadMax];
-    __shared__ float red_f[kAttnThreads / kWave];
-    __shared__ int red_i[kAttnThreads / kWave];
-    __shared__ double lane_sum[8];
-    __shared__ double tail_e[8];
-    __shared__ float inv_s;
-    const int head = blockIdx.x;
-    const int rep = n_heads / n_kv, g = head / rep;
-    // A decode step: the position in DecodeState.  A prompt chunk: row blockIdx.y of qkv / out
-    // at position pos_first + blockIdx.y (every row's k and v already in the cache).
-    const int pos = pos_first >= 0 ? pos_first + static_cast<int>(blockIdx.y) : st->pos, T = pos + 1;
-    qkv += static_cast<size_t>(blockIdx.y) * qkv_stride;
-    out += static_cast<size_t>(blockIdx.y) * out_stride;
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    constexpr int kWaves = kAttnThreads / kWave;
-    float* ktile = sc + ((cap + 3) & ~3);   // tile * hd
-    float* vtile = ktile + tile * hd;       // tile * hd
-    float* dump = vtile + tile * hd;        // 4 floats: where stores past a tile's end go
-    float* K = kc + static_cast<size_t>(g) * cap * hd;
-    float* V = vc + static_cast<size_t>(g) * cap * hd;
-    // This step's q, k, v and the first round's cached K and V (positions < pos), all loads
-    // issued before any store.
-    const int first_cached = min(min(tile, T), pos);
-    {
-        // q, k, v loaded by every thread (a clamped index past head_dim; qs, ks, vs hold
-        // kHeadMax entries, of which the first hd are read) and stored after the tiles, so
-        // their loads are not waited for before the tile loads are issued.
-        const int d = min(static_cast<int>(threadIdx.x), hd - 1);
-        const float q0 = qkv[static_cast<size_t>(head) * hd + d];
-        const float k0 = qkv[static_cast<size_t>(n_heads + g) * hd + d];
-        const float v0 = qkv[static_cast<size_t>(n_heads + n_kv + g) * hd + d];
-        stage_tiles<true>(ktile, K, vtile, V, first_cached * hd, dump);
-        if (threadIdx.x < kHeadMax) {
-            qs[threadIdx.x] = q0;
-            ks[threadIdx.x] = k0;
-            vs[threadIdx.x] = v0;
-        }
-    }
-    __syncthreads();
-    const float* cs = cos_tab + static_cast<size_t>(pos) * hd;
-    const float* sn = sin_tab + static_cast<size_t>(pos) * hd;
-    rope_head_lds(qs, cs, sn, hd, interleaved);
-    rope_head_lds(ks, cs, sn, hd, interleaved);
-    __syncthreads();
-    if (head % rep == 0)
-        for (int d = threadIdx.x; d < hd; d += kAttnThreads) {
-            K[static_cast<size_t>(pos) * hd + d] = ks[d];
-            V[static_cast<size_t>(pos) * hd + d] = vs[d];
-        }
-    // Scores and the V tiles, `tile` positions a round.  Position pos comes from ks / vs.
-    const int l = threadIdx.x & 15;
-    for (int t0 = 0; t0 < T; t0 += tile) {
-        const int tn = min(tile, T - t0);
-        const int cached = min(tn, pos - t0);  // positions of this round read from the cache
-        __syncthreads();  // the previous round's tiles are consumed
-        if (cached > 0 && t0 > 0) stage_tiles<false>(ktile, K + static_cast<size_t>(t0) * hd, nullptr, nullptr, cached * hd, dump);
-        if (cached < tn)
-            for (int d = threadIdx.x; d < hd; d += kAttnThreads) ktile[(pos - t0) * hd + d] = ks[d];
-        __syncthreads();
-        for (int tb = 0; tb < tn; tb += kAttnThreads / 16) {  // uniform bound: every lane reaches the DPP
-            const int tt = tb + (threadIdx.x >> 4);
-            const int tc = min(tt, tn - 1);
-            const float* kr = ktile + tc * hd;
-            float a0 = 0.0f, a1 = 0.0f;
-            for (int p = 0; p < hd; p += 32) {
-                if (p + l < hd) a0 = fmaf(qs[p + l], kr[p + l], a0);
-                if (p + 16 + l < hd) a1 = fmaf(qs[p + 16 + l], kr[p + 16 + l], a1);
-            }
-            // Lane 0 of the 16 gets ((s0 + s8) + (s4 + s12)) + ... as the reference's halving
-            // reduce (lanes i and i+8, then i+4, i+2, i+1), the partners read through DPP.
-            float v = a0 + a1;
-            v = v + dpp_f<kDppRowShl8>(v);
-            v = v + dpp_f<kDppRowShl4>(v);
-            v = v + dpp_f<kDppRowShl2>(v);
-            v = v + dpp_f<kDppRowShl1>(v);
-            if (l == 0 && tt < tn) sc[t0 + tt] = scale * v;
-        }
-    }
-    __syncthreads();
-    // Softmax over the T scores.
-    float mx = -__builtin_inff();
-    int nonfinite = 0;
-    for (int t = threadIdx.x; t < T; t += kAttnThreads) {
-        const uint32_t u = __float_as_uint(sc[t]);
-        nonfinite |= (u & 0x7fffffffu) > 0x7f800000u || u == 0x7f800000u;
-        mx = fmaxf(mx, sc[t]);
-    }
-    mx = group_max<kWave>(mx);
-    nonfinite = group_sum_int<kWave>(nonfinite);
-    if (lane == 0) {
-        red_f[wave] = mx;
-        red_i[wave] = nonfinite;
-    }
-    __syncthreads();
-    mx = red_f[0];
-    nonfinite = red_i[0];
-    for (int w = 1; w < kWaves; ++w) {
-        mx = fmaxf(mx, red_f[w]);
-        nonfinite |= red_i[w];
-    }
-    const bool nan_row = nonfinite || __float_as_uint(mx) == 0xff800000u;
-    const int n8 = T - T % 8;
-    for (int t = threadIdx.x; t < T; t += kAttnThreads) {
-        const float dd = sc[t] - mx;
-        if (t < n8) {
-            sc[t] = exp_cody_waite(dd);
-        } else {
-            const double e = exp(static_cast<double>(dd));
-            tail_e[t - n8] = e;
-            sc[t] = static_cast<float>(e);
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x < 8) {
-        double acc = 0.0;
-        for (int t = threadIdx.x; t < n8; t += 8) acc = acc + static_cast<double>(sc[t]);
-        lane_sum[threadIdx.x] = acc;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        double tsum = lane_sum[0];
-        for (int k = 1; k < 8; ++k) tsum = tsum + lane_sum[k];
-        double sum = 0.0 + tsum;
-        for (int t = 0; t < T - n8; ++t) sum = sum + tail_e[t];
-        inv_s = static_cast<float>(1.0 / sum);
-    }
-    __syncthreads();
-    const float inv = inv_s;
-    for (int t = threadIdx.x; t < T; t += kAttnThreads) sc[t] = nan_row ? __builtin_nanf("") : sc[t] * inv;
-    // out[d] = one fused chain over the positions in order.
-    float acc = 0.0f;
-    const int d = threadIdx.x;
-    for (int t0 = 0; t0 < T; t0 += tile) {
-        const int tn = min(tile, T - t0);
-        const int cached = min(tn, pos - t0);
-        __syncthreads();  // probabilities written / the previous tile consumed
-        if (cached > 0 && t0 > 0) stage_tiles<false>(vtile, V + static_cast<size_t>(t0) * hd, nullptr, nullptr, cached * hd, dump);
-        if (cached < tn)
-            for (int e = threadIdx.x; e < hd; e += kAttnThreads) vtile[(pos - t0) * hd + e] = vs[e];
-        __syncthreads();
-        if (d < hd) {
-#pragma unroll 8
-            for (int t = 0; t < tn; ++t) acc = fmaf(sc[t0 + t], vtile[t * hd + d], acc);
-        }
-    }
-    if (d < hd) out[static_cast<size_t>(head) * hd + d] = acc;
-}
-
-// Positions per round: the whole cache when it fits kMaxTile, else as many as the LDS budget
-// leaves beside the scores (at least 16).
-int attention_tile(int cap, int hd) {
-    const size_t left = kAttnLdsBudget / 4 - static_cast<size_t>((cap + 3) & ~3) - 4;  // 4: the spare slot
-    const int fit = static_cast<int>(left / (2 * static_cast<size_t>(hd)));
-    return std::max(16, std::min({kMaxTile, cap, fit}));
-}
-size_t attention_lds(int cap, int hd) {
-    return (static_cast<size_t>((cap + 3) & ~3) + 2 * static_cast<size_t>(attention_tile(cap, hd)) * hd + 4) * 4;
 }
 
 // Prompt chunk: k = rope(k) and v of rows p < gridDim.y into the cache at pos_first + p, for KV
@@ -602,7 +705,7 @@ hipError_t enqueue_step(Model& md, bool with_logits, Marks* mk = nullptr) {
         hipError_t e = gemv_normed(md, L.qkv, md.x, L.attn_norm, md.h, md.qkv, false);
         if (e != hipSuccess) return e;
         SMK_MARK(kAttention);
-        hipLaunchKernelGGL(attention_kernel, dim3(nh), dim3(kAttnThreads), attention_lds(md.capacity, hd), s,
+        hipLaunchKernelGGL(attention_for(hd), dim3(nh), dim3(kAttnThreads), attention_lds(md.capacity, hd), s,
                            md.qkv, md.cos_tab, md.sin_tab, c.rope_interleaved, kc, vc, nh, nkv, hd, md.capacity,
                            scale, attention_tile(md.capacity, hd), md.st, md.attn, -1, 0, 0);
         if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -693,7 +796,7 @@ hipError_t enqueue_prompt_chunk(Model& md, int first, int P, bool with_logits) {
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(rope_kv_kernel, dim3(nkv, P), dim3(kRopeKvThreads), 0, s, md.bqkv, qkv_rows, md.cos_tab,
                            md.sin_tab, c.rope_interleaved, kc, vc, nh, nkv, hd, md.capacity, first);
-        hipLaunchKernelGGL(attention_kernel, dim3(nh, P), dim3(kAttnThreads), attention_lds(md.capacity, hd), s,
+        hipLaunchKernelGGL(attention_for(hd), dim3(nh, P), dim3(kAttnThreads), attention_lds(md.capacity, hd), s,
                            md.bqkv, md.cos_tab, md.sin_tab, c.rope_interleaved, kc, vc, nh, nkv, hd, md.capacity,
                            scale, attention_tile(md.capacity, hd), md.st, md.battn, first, qkv_rows, md.q_rows());
         if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -944,7 +1047,7 @@ int smk_llama_reset(void* model, int capacity, const float* cos_table, const flo
     SMK_HIP(hipStreamSynchronize(md->stream), "reset");
     md->pos = 0;
     if (!md->g_logits) {
-        SMK_HIP(allow_lds(attention_kernel, attention_lds(capacity, md->cfg.head_dim)), "attention LDS");
+        SMK_HIP(allow_lds(attention_for(md->cfg.head_dim), attention_lds(capacity, md->cfg.head_dim)), "attention LDS");
         SMK_HIP(capture(*md, true, &md->g_logits), "capture step");
         SMK_HIP(capture(*md, false, &md->g_plain), "capture step (no logits)");
     }
