@@ -1290,11 +1290,14 @@ hipError_t launch_ordered_ch(int M, int N, int K, const float* x, int ldx, const
         // weights leave the activations and the KV cache in the caches.
         const int groups = (rows_per_wg + kRows - 1) / kRows;
         const int forced = g_q4_stream.load();
-        const int mode = !st ? 0 : forced > 0 ? forced : groups >= 8 ? 2 : nrm.stream ? 1 : 0;
+        const int mode0 = !st ? 0 : forced > 0 ? forced : groups >= 8 ? 2 : nrm.stream ? 1 : 0;
+        const int mode = NT == 1024 && mode0 == 2 ? 1 : mode0;  // (two groups ahead spill at 1024 threads)
 #define SMK_ORDERED(S, NORM) \
     launch_ordered_kernel<LPR, MT, NT, CH, S, NORM>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, nbuf, bytes, stream)
-        if (nrm.w) return mode == 2 ? SMK_ORDERED(2, true) : mode == 1 ? SMK_ORDERED(1, true) : SMK_ORDERED(0, true);
-        if (mode == 2) return SMK_ORDERED(2, false);
+        if constexpr (NT < 1024) {
+            if (mode == 2) return nrm.w ? SMK_ORDERED(2, true) : SMK_ORDERED(2, false);
+        }
+        if (nrm.w) return mode == 1 ? SMK_ORDERED(1, true) : SMK_ORDERED(0, true);
         if (mode == 1) return SMK_ORDERED(1, false);
 #undef SMK_ORDERED
     } else {
@@ -1309,10 +1312,22 @@ template <int LPR, int MT, int NT>
 hipError_t launch_ordered(int M, int N, int K, const float* x, int ldx, const uint8_t* W, float* y, int ldy,
                           int rows_per_wg, int acc, hipStream_t stream, const NormArgs& nrm = NormArgs()) {
     const int chunks = ((K >> 6) + LPR - 1) / LPR;
-    if (chunks <= 1) return launch_ordered_ch<LPR, MT, NT, 1>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
-    if (chunks <= 2) return launch_ordered_ch<LPR, MT, NT, 2>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
-    if (chunks <= 4) return launch_ordered_ch<LPR, MT, NT, 4>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
-    return hipErrorInvalidValue;
+    if constexpr (NT == 1024) {
+        // 128 registers a lane: only one pair a lane and row, at least 16 lanes a row, and at
+        // most one group in flight fit without spilling (the build checks it).
+        if constexpr (LPR < 16) {
+            return hipErrorInvalidValue;
+        } else {
+            if (chunks <= 1)
+                return launch_ordered_ch<LPR, MT, NT, 1>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
+            return hipErrorInvalidValue;
+        }
+    } else {
+        if (chunks <= 1) return launch_ordered_ch<LPR, MT, NT, 1>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
+        if (chunks <= 2) return launch_ordered_ch<LPR, MT, NT, 2>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
+        if (chunks <= 4) return launch_ordered_ch<LPR, MT, NT, 4>(M, N, K, x, ldx, W, y, ldy, rows_per_wg, acc, nrm, stream);
+        return hipErrorInvalidValue;
+    }
 }
 
 template <int MT, int NT>
@@ -1468,16 +1483,18 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
         int nt = (t && t->threads) ? t->threads : 256;
         const size_t cap = kLdsCap - (nrm.w ? (static_cast<size_t>(K) + (8u << nrm.depth)) * 4 : 0);
         if (!(t && t->threads)) {
-            while (nt < 512 && nt < rpw * lpr) nt *= 2;
+            while (nt < 1024 && nt < rpw * lpr) nt *= 2;
+            if (nt == 1024 && (lpr < 16 || pairs > lpr)) nt = 512;  // the 1024-thread forms that fit
             while (nt > 256 && ordered_lds_bytes(1, K, nt / lpr) > cap) nt /= 2;
         }
         while (ordered_lds_bytes(1, K, nt / lpr) > cap && lpr < (nrm.silu_pairs ? 32 : 64)) lpr *= 2;
         if (nrm.w)  // eight lanes per leaf of the norm's tree, at most four quads of x per thread
             while (nt < (8 << nrm.depth) || nt * 16 < K) nt *= 2;
         switch (nt) {
+            case 1024: return launch_ordered_lpr<1, 1024>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream, nrm);
             case 512: return launch_ordered_lpr<1, 512>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream, nrm);
             case 256: return launch_ordered_lpr<1, 256>(lpr, M, N, K, x, ldx, W, y, ldy, rpw, acc, stream, nrm);
-            default: return hipErrorInvalidValue;  // 1024 threads: no room for the row groups' registers
+            default: return hipErrorInvalidValue;
         }
     }
     // Several rows of x: 256 threads, 32 or 64 lanes per row (phase 2 needs 4 * rows * M <= 256).
