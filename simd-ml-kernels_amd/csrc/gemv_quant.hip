@@ -415,6 +415,7 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ int bad[MT];
     __shared__ float wave_sum[NT / kWave];
+    __shared__ float norm_scale;
 
     const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
     const int S = ordered_stride(nb);
@@ -527,6 +528,15 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
             xr[u] = x4[c];
             wr[u] = w4[c];
         }
+        // K = 2048 (16 leaves of 128): wave 0 also loads the whole of x and computes the mean of
+        // squares alone (wave_sumsq_2048), so that no other wave waits for it but once, for the
+        // scale; other widths go through LDS (uniform_chunk_sum).
+        const bool wave_norm = K == 2048 && norm_depth == 4;
+        float4 xw[8];
+        if (wave_norm && wave == 0) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) xw[u] = x4[lane * 8 + u];
+        }
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_sched_barrier(0);
         // Every wave issues its x loads before any wave issues weight loads: a CU's vector loads
@@ -536,18 +546,29 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
         __builtin_amdgcn_sched_barrier(0);
         first_loads();
         __builtin_amdgcn_sched_barrier(0);
-        // x into LDS with 8 spare floats after every leaf of the pairwise tree (leaves of
-        // K >> depth values: the host checks they are equal), read back conflict-free by the sum.
-        const int leaf = K >> norm_depth;
+        float scale;
+        if (wave_norm) {
+            if (wave == 0) {
+                const float total = wave_sumsq_2048(xw);
+                const float var = static_cast<float>(static_cast<double>(total) / static_cast<double>(K));
+                if (lane == 0) norm_scale = static_cast<float>(1.0 / sqrt(static_cast<double>(var) + norm_eps));
+            }
+            lds_barrier();
+            scale = norm_scale;
+        } else {
+            // x into LDS with 8 spare floats after every leaf of the pairwise tree (leaves of
+            // K >> depth values: the host checks they are equal), read back conflict-free by the sum.
+            const int leaf = K >> norm_depth;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int qd = static_cast<int>(threadIdx.x) + u * NT;
-            if (qd < quads) reinterpret_cast<float4*>(xf + 8 * ((4 * qd) / leaf))[qd] = xr[u];
+            for (int u = 0; u < 4; ++u) {
+                const int qd = static_cast<int>(threadIdx.x) + u * NT;
+                if (qd < quads) reinterpret_cast<float4*>(xf + 8 * ((4 * qd) / leaf))[qd] = xr[u];
+            }
+            lds_barrier();
+            const float total = uniform_chunk_sum<NT>(xf, K, norm_depth, wave_sum, 8);
+            const float var = static_cast<float>(static_cast<double>(total) / static_cast<double>(K));
+            scale = static_cast<float>(1.0 / sqrt(static_cast<double>(var) + norm_eps));
         }
-        lds_barrier();
-        const float total = uniform_chunk_sum<NT>(xf, K, norm_depth, wave_sum, 8);
-        const float var = static_cast<float>(static_cast<double>(total) / static_cast<double>(K));
-        const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(var) + norm_eps));
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             if (u * NT >= quads) break;  // uniform: no thread has a quad this far
