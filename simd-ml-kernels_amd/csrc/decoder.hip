@@ -217,8 +217,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     __shared__ double tail_e[8];
     __shared__ float inv_s;
     const int hd = HD > 0 ? HD : hd_arg, kst = k_stride(hd);
-    const int head = blockIdx.x;
-    const int rep = n_heads / n_kv, g = head / rep;
+    // Workgroup b takes KV group b % n_kv: the workgroups of one group are n_kv apart, and with
+    // workgroups dealt to the XCDs in turn (8 on MI355X) they share an XCD, and so its L2, when
+    // n_kv is a multiple of 8 -- the group's K and V then come from HBM once, not once per head.
+    const int rep = n_heads / n_kv, g = static_cast<int>(blockIdx.x) % n_kv;
+    const int head = g * rep + static_cast<int>(blockIdx.x) / n_kv;
     // A decode step: the position in DecodeState.  A prompt chunk: row blockIdx.y of qkv / out
     // at position pos_first + blockIdx.y (every row's k and v already in the cache).
     const int pos = pos_first >= 0 ? pos_first + static_cast<int>(blockIdx.y) : st->pos, T = pos + 1;
