@@ -44,30 +44,44 @@ struct DecodeState {
 // ─── kernels ────────────────────────────────────────────────────────────────
 
 // x = row `token` of the embedding (llama.py:337 / gguf_reader.py:112-129: d * (q - 8) for
-// Q4_0, d * q for Q8_0, the float32 row for F32; every product is exact in float32).
+// Q4_0, d * q for Q8_0, the float32 row for F32; every product is exact in float32).  One thread
+// per 32-value block: all 2-byte reads of the block are issued before any value is formed (GGUF
+// blocks are 2-byte aligned), so a row costs one memory latency, not one per value.
 __device__ __forceinline__ void embed_row(const uint8_t* __restrict__ E, int type, int hidden, int vocab, int tok,
                                           float* __restrict__ x) {
     tok = min(max(tok, 0), vocab - 1);  // host checks every token; a bad one must not fault
-    const int nb = hidden >> 5;
-    for (int i = threadIdx.x; i < hidden; i += blockDim.x) {
-        float v;
-        if (type == kGgmlF32) {
-            v = reinterpret_cast<const float*>(E)[static_cast<size_t>(tok) * hidden + i];
-        } else {
-            const int b = i >> 5, j = i & 31;
-            const int bb = type == kGgmlQ4_0 ? kQ4_0Bytes : kQ8_0Bytes;
-            const uint8_t* blk = E + (static_cast<size_t>(tok) * nb + b) * bb;
-            const float d = half_bits_to_float(static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8));
-            int q;
-            if (type == kGgmlQ4_0) {
-                const int byte = blk[2 + (j & 15)];
-                q = (j < 16 ? (byte & 15) : (byte >> 4)) - 8;
-            } else {
-                q = static_cast<int8_t>(blk[2 + j]);
+    if (type == kGgmlF32) {  // any width
+        const float* src = reinterpret_cast<const float*>(E) + static_cast<size_t>(tok) * hidden;
+        for (int i = threadIdx.x; i < hidden; i += blockDim.x) x[i] = src[i];
+        return;
+    }
+    const int nb = hidden >> 5;  // quantized rows are whole blocks
+    for (int b = threadIdx.x; b < nb; b += blockDim.x) {
+        float v[32];
+        if (type == kGgmlQ4_0) {
+            const uint16_t* blk = reinterpret_cast<const uint16_t*>(E + (static_cast<size_t>(tok) * nb + b) * kQ4_0Bytes);
+            uint16_t h[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) h[k] = blk[k];
+            const float d = half_bits_to_float(h[0]);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int byte = (h[1 + (j >> 1)] >> (8 * (j & 1))) & 0xff;
+                v[j] = d * static_cast<float>((byte & 15) - 8);
+                v[16 + j] = d * static_cast<float>((byte >> 4) - 8);
             }
-            v = d * static_cast<float>(q);
+        } else {
+            const uint16_t* blk = reinterpret_cast<const uint16_t*>(E + (static_cast<size_t>(tok) * nb + b) * kQ8_0Bytes);
+            uint16_t h[17];
+#pragma unroll
+            for (int k = 0; k < 17; ++k) h[k] = blk[k];
+            const float d = half_bits_to_float(h[0]);
+#pragma unroll
+            for (int j = 0; j < 32; ++j)
+                v[j] = d * static_cast<float>(static_cast<int8_t>((h[1 + (j >> 1)] >> (8 * (j & 1))) & 0xff));
         }
-        x[i] = v;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) x[32 * b + j] = v[j];
     }
 }
 
