@@ -240,23 +240,22 @@ __global__ __launch_bounds__(kThreads) void rms_norm_uniform_kernel(const float*
 // depth 4), no LDS and no barrier.
 __global__ __launch_bounds__(kWave) void rms_norm_2048_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                               float* __restrict__ y, double eps) {
-    const int lane = static_cast<int>(threadIdx.x);
-    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(blockIdx.x) * 2048) + 8 * lane;
-    const float4* wr = reinterpret_cast<const float4*>(w) + 8 * lane;
-    float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(blockIdx.x) * 2048) + 8 * lane;
-    float4 xv[8], wv[8];
+    const float* xr = x + static_cast<size_t>(blockIdx.x) * 2048;
+    float* yr = y + static_cast<size_t>(blockIdx.x) * 2048;
+    float2 xs[16], ws[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        xv[u] = xr[u];
-        wv[u] = wr[u];
+    for (int j = 0; j < 16; ++j) {
+        const int i = wave_sumsq_index(j);
+        xs[j] = *reinterpret_cast<const float2*>(xr + i);
+        ws[j] = *reinterpret_cast<const float2*>(w + i);
     }
-    const float total = -0.0f + wave_sumsq_2048(xv);
+    const float total = -0.0f + wave_sumsq_2048(xs);
     const float var = static_cast<float>(static_cast<double>(total) / 2048.0);
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(var) + eps));
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-        yr[u] = make_float4(wv[u].x * (xv[u].x * scale), wv[u].y * (xv[u].y * scale), wv[u].z * (xv[u].z * scale),
-                            wv[u].w * (xv[u].w * scale));
+    for (int j = 0; j < 16; ++j)
+        *reinterpret_cast<float2*>(yr + wave_sumsq_index(j)) =
+            make_float2(ws[j].x * (xs[j].x * scale), ws[j].y * (xs[j].y * scale));
 }
 
 // x [heads, head_dim] -> y; cos/sin [head_dim] (halves equal, as rope_cos_sin makes them).
@@ -304,8 +303,8 @@ hipError_t softmax_rows(const float* in, float* out, int rows, int n, hipStream_
 
 hipError_t rms_norm(const float* x, const float* w, float* y, int rows, int n, double eps, hipStream_t s) {
     if (rows <= 0 || n <= 0) return hipSuccess;
-    if (n == 2048 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
-        reinterpret_cast<uintptr_t>(y) % 16 == 0) {
+    if (n == 2048 && reinterpret_cast<uintptr_t>(x) % 8 == 0 && reinterpret_cast<uintptr_t>(w) % 8 == 0 &&
+        reinterpret_cast<uintptr_t>(y) % 8 == 0) {
         hipLaunchKernelGGL(rms_norm_2048_kernel, dim3(rows), dim3(kWave), 0, s, x, w, y, eps);
         return hipGetLastError();
     }

@@ -531,11 +531,11 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
         // K = 2048 (16 leaves of 128): wave 0 also loads the whole of x and computes the mean of
         // squares alone (wave_sumsq_2048), so that no other wave waits for it but once, for the
         // scale; other widths go through LDS (uniform_chunk_sum).
-        const bool wave_norm = K == 2048 && norm_depth == 4;
-        float4 xw[8];
+        const bool wave_norm = K == 2048 && norm_depth == 4 && reinterpret_cast<uintptr_t>(x) % 8 == 0;
+        float2 xw[16];
         if (wave_norm && wave == 0) {
 #pragma unroll
-            for (int u = 0; u < 8; ++u) xw[u] = x4[lane * 8 + u];
+            for (int j = 0; j < 16; ++j) xw[j] = *reinterpret_cast<const float2*>(x + wave_sumsq_index(j));
         }
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_sched_barrier(0);

@@ -90,53 +90,34 @@ __device__ __forceinline__ float uniform_chunk_sum(const float* __restrict__ q, 
 }
 
 
-// numpy's pairwise sum of the squares of 2048 values held by one wave (lane L: values 32L ..
-// 32L + 31 in xw), with no LDS and no workgroup barrier.  The tree over 2048 values has 16 leaves
-// of 128 (every split exact); leaf l is lanes 4l .. 4l + 3, lane 4l + p holding its values
-// 32p .. 32p + 31, i.e. steps j = 4p .. 4p + 3 of the leaf's eight interleaved accumulators
-// (accumulator k adds x[8j + k]^2 for j = 0, 1, ... in order, starting from x[k]^2).  The
-// accumulators run through the four lanes of a leaf in turn (three hand-overs), then
-// ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) on the leaf's last lane, and the leaves add level by level
-// (lanes xor 4, 8, 16, 32: leaf l with leaf l ^ 1, then pairs of pairs).  Every lane returns
-// the total.  Same operations and order as uniform_chunk_sum at depth 4.
-__device__ __forceinline__ float wave_sumsq_2048(const float4 (&xw)[8]) {
-    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1), p = lane & 3;
-    float sq[32];
+// numpy's pairwise sum of the squares of 2048 values held by one wave, with no LDS and no
+// workgroup barrier.  The tree over 2048 values has 16 leaves of 128 (every split exact); leaf l
+// is lanes 4l .. 4l + 3, and lane 4l + m holds accumulators 2m and 2m + 1 of the leaf's eight
+// (accumulator k adds x[8j + k]^2 for j = 0 .. 15 in order, starting from x[k]^2): xs[j] =
+// (x[128 l + 8 j + 2 m], x[128 l + 8 j + 2 m + 1]) -- see wave_sumsq_index.  Each lane runs its
+// two chains alone; then ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) by exchanges inside the quad, and
+// the leaves add level by level (lanes xor 4, 8, 16, 32: leaf l with leaf l ^ 1, then pairs of
+// pairs).  Every lane returns the total.  Same operations and order as uniform_chunk_sum at
+// depth 4.
+__device__ __forceinline__ int wave_sumsq_index(int j) {
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    return 128 * (lane >> 2) + 8 * j + 2 * (lane & 3);
+}
+__device__ __forceinline__ float wave_sumsq_2048(const float2 (&xs)[16]) {
+    float r0 = xs[0].x * xs[0].x, r1 = xs[0].y * xs[0].y;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        sq[4 * u + 0] = xw[u].x * xw[u].x;
-        sq[4 * u + 1] = xw[u].y * xw[u].y;
-        sq[4 * u + 2] = xw[u].z * xw[u].z;
-        sq[4 * u + 3] = xw[u].w * xw[u].w;
+    for (int j = 1; j < 16; ++j) {
+        r0 = r0 + xs[j].x * xs[j].x;
+        r1 = r1 + xs[j].y * xs[j].y;
     }
-    float r[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) r[k] = sq[k];  // the leaf's first lane (p == 0) starts at x[k]^2
-#pragma unroll
-    for (int j = 1; j < 4; ++j)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) r[k] = r[k] + sq[8 * j + k];
-#pragma unroll
-    for (int s = 1; s < 4; ++s) {  // lane p == s continues the chains of lane p - 1
-        float prev[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) prev[k] = __shfl(r[k], (lane + kWave - 1) & (kWave - 1), kWave);
-        if (p == s) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                float a = prev[k];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) a = a + sq[8 * j + k];
-                r[k] = a;
-            }
-        }
-    }
-    float t = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));  // valid where p == 3
+    float t = r0 + r1;                          // r(2m) + r(2m+1)
+    t = t + __shfl_xor(t, 1, kWave);            // (r0+r1)+(r2+r3), (r4+r5)+(r6+r7)
+    t = t + __shfl_xor(t, 2, kWave);            // the leaf
     t = t + __shfl_xor(t, 4, kWave);
     t = t + __shfl_xor(t, 8, kWave);
     t = t + __shfl_xor(t, 16, kWave);
     t = t + __shfl_xor(t, 32, kWave);
-    return __shfl(t, 3, kWave);
+    return t;
 }
 
 // Depth at which every leaf of numpy's pairwise tree over len values sits, or -1 when the
