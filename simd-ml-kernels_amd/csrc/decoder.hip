@@ -548,9 +548,13 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_part_kernel(const float
     }
 }
 
+// ... and x = the embedding row of the next step's token (the prompt's next token, or the
+// argmax past the prompt), so that a decode step that follows needs no embedding launch.
 __global__ __launch_bounds__(kWave) void argmax_final_kernel(const float* __restrict__ pv, const int* __restrict__ pi,
                                                              int parts, int n, int* __restrict__ tokens, int cap,
-                                                             DecodeState* __restrict__ st) {
+                                                             DecodeState* __restrict__ st, const uint8_t* __restrict__ E,
+                                                             int etype, int hidden, float* __restrict__ x) {
+    const int p = st->pos, n_prompt = st->n_prompt;  // read by every lane before lane 0 advances pos
     float v = -__builtin_inff();
     int idx = 0x7fffffff;
     for (int b = threadIdx.x; b < parts; b += kWave)
@@ -558,13 +562,13 @@ __global__ __launch_bounds__(kWave) void argmax_final_kernel(const float* __rest
             v = pv[b];
             idx = pi[b];
         }
-    argmax_wave(v, idx);
+    argmax_wave(v, idx);  // every lane holds the result
+    if (idx < 0 || idx >= n) idx = 0;  // n == 0 cannot happen (vocab > 0)
     if (threadIdx.x == 0) {
-        if (idx < 0 || idx >= n) idx = 0;  // n == 0 cannot happen (vocab > 0)
-        const int p = st->pos;
-        if (p + 1 >= st->n_prompt && p + 1 <= cap) tokens[p + 1] = idx;
+        if (p + 1 >= n_prompt && p + 1 <= cap) tokens[p + 1] = idx;
         st->pos = p + 1;
     }
+    if (p + 1 <= cap) embed_row(E, etype, hidden, n, p + 1 < n_prompt ? tokens[p + 1] : idx, x);
 }
 
 __global__ void advance_kernel(DecodeState* st) {
@@ -633,6 +637,7 @@ struct Model {
     int* tokens = nullptr;
     float *kc = nullptr, *vc = nullptr, *cos_tab = nullptr, *sin_tab = nullptr;
     hipGraphExec_t g_logits = nullptr, g_plain = nullptr;
+    hipGraphExec_t g_next = nullptr;  // a logits step whose embedding the previous step's argmax wrote
     std::vector<unsigned> loaded;  // bit per tensor per layer
     bool fuse_norm = false;        // Q4_0 GEMVs normalize x themselves
     bool fuse_silu = false;        // gate/up rows interleaved; the GEMV writes silu(gate) * up
@@ -659,7 +664,8 @@ hipError_t dalloc(Model& md, void** p, size_t bytes) {
 void free_capacity(Model& md) {
     if (md.g_logits) (void)hipGraphExecDestroy(md.g_logits);
     if (md.g_plain) (void)hipGraphExecDestroy(md.g_plain);
-    md.g_logits = md.g_plain = nullptr;
+    if (md.g_next) (void)hipGraphExecDestroy(md.g_next);
+    md.g_logits = md.g_plain = md.g_next = nullptr;
     for (void* p : {static_cast<void*>(md.tokens), static_cast<void*>(md.kc), static_cast<void*>(md.vc),
                     static_cast<void*>(md.cos_tab), static_cast<void*>(md.sin_tab)})
         if (p) (void)hipFree(p);
@@ -704,14 +710,17 @@ hipError_t gemv(const Mat& W, const float* x, float* y, bool accumulate, hipStre
             if (const hipError_t e_ = mk->mark(s, section); e_ != hipSuccess) return e_; \
     } while (0)
 
-hipError_t enqueue_step(Model& md, bool with_logits, Marks* mk = nullptr) {
+// embed = false: x already holds the step's embedding row (the previous step's argmax wrote it).
+hipError_t enqueue_step(Model& md, bool with_logits, Marks* mk = nullptr, bool embed = true) {
     const smk_llama_config& c = md.cfg;
     hipStream_t s = md.stream;
     const int nh = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
     SMK_MARK(kEmbed);
-    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, md.embed.p, md.embed.type, c.hidden, c.vocab,
-                       md.tokens, md.st, md.x);
-    if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    if (embed) {
+        hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, md.embed.p, md.embed.type, c.hidden, c.vocab,
+                           md.tokens, md.st, md.x);
+        if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    }
     const size_t layer_kv = static_cast<size_t>(nkv) * md.capacity * hd;
     const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(hd)));
     for (int l = 0; l < c.n_layers; ++l) {
@@ -755,7 +764,7 @@ hipError_t enqueue_step(Model& md, bool with_logits, Marks* mk = nullptr) {
     hipLaunchKernelGGL(argmax_part_kernel, dim3(kArgmaxParts), dim3(kArgmaxThreads), 0, s, md.logits, c.vocab,
                        md.part_v, md.part_i);
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kWave), 0, s, md.part_v, md.part_i, kArgmaxParts, c.vocab,
-                       md.tokens, md.capacity, md.st);
+                       md.tokens, md.capacity, md.st, md.embed.p, md.embed.type, c.hidden, md.x);
     return hipGetLastError();
 }
 #undef SMK_MARK
@@ -838,14 +847,14 @@ hipError_t enqueue_prompt_chunk(Model& md, int first, int P, bool with_logits) {
     hipLaunchKernelGGL(argmax_part_kernel, dim3(kArgmaxParts), dim3(kArgmaxThreads), 0, s, md.logits, c.vocab,
                        md.part_v, md.part_i);
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kWave), 0, s, md.part_v, md.part_i, kArgmaxParts, c.vocab,
-                       md.tokens, md.capacity, md.st);
+                       md.tokens, md.capacity, md.st, md.embed.p, md.embed.type, c.hidden, md.x);
     return hipGetLastError();
 }
 
-hipError_t capture(Model& md, bool with_logits, hipGraphExec_t* out) {
+hipError_t capture(Model& md, bool with_logits, hipGraphExec_t* out, bool embed = true) {
     hipError_t e = hipStreamBeginCapture(md.stream, hipStreamCaptureModeThreadLocal);
     if (e != hipSuccess) return e;
-    const hipError_t body = enqueue_step(md, with_logits);
+    const hipError_t body = enqueue_step(md, with_logits, nullptr, embed);
     hipGraph_t graph = nullptr;
     e = hipStreamEndCapture(md.stream, &graph);
     if (body != hipSuccess) {
@@ -1070,6 +1079,7 @@ int smk_llama_reset(void* model, int capacity, const float* cos_table, const flo
         SMK_HIP(allow_lds(attention_for(md->cfg.head_dim), attention_lds(capacity, md->cfg.head_dim)), "attention LDS");
         SMK_HIP(capture(*md, true, &md->g_logits), "capture step");
         SMK_HIP(capture(*md, false, &md->g_plain), "capture step (no logits)");
+        SMK_HIP(capture(*md, true, &md->g_next, false), "capture step (embedded by the last argmax)");
     }
     return ok();
 }
@@ -1149,7 +1159,8 @@ int smk_llama_generate(void* model, const int* prompt, int n_prompt, int n_new, 
         for (int i = 0; i < n_prompt; ++i) SMK_HIP(hipGraphLaunch(md->g_logits, md->stream), "prefill graph");
     }
     SMK_HIP(hipEventRecord(md->ev[1], md->stream), "event");
-    for (int i = 0; i < n_new - 1; ++i) SMK_HIP(hipGraphLaunch(md->g_logits, md->stream), "decode graph");
+    // Every prompt form ends with an argmax, which wrote the first decode step's embedding.
+    for (int i = 0; i < n_new - 1; ++i) SMK_HIP(hipGraphLaunch(md->g_next, md->stream), "decode graph");
     SMK_HIP(hipEventRecord(md->ev[2], md->stream), "event");
     SMK_HIP(hipMemcpyAsync(out, md->tokens + n_prompt, static_cast<size_t>(n_new) * 4, hipMemcpyDeviceToHost,
                            md->stream),
