@@ -167,29 +167,38 @@ __device__ __forceinline__ uint32_t q8_quad(const float (&v)[4], float& d, int (
            ((static_cast<uint32_t>(q[2]) & 0xffu) << 16) | (static_cast<uint32_t>(q[3]) << 24);
 }
 
+// The low bytes of four ints as one dword, q0 in the low byte.
+__device__ __forceinline__ uint32_t pack_low_bytes(int q0, int q1, int q2, int q3) {
+    const uint32_t lo = __builtin_amdgcn_perm(static_cast<uint32_t>(q1), static_cast<uint32_t>(q0), 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(static_cast<uint32_t>(q3), static_cast<uint32_t>(q2), 0x04000c0cu);
+    return lo | hi;
+}
+
 // Q8 quants of two quads of x, k and k + 4 (values 4k..4k+3 and 16+4k..16+4k+3) of a
-// 32-value block whose four lanes (k = 0..3) call this together: the same arithmetic as q8_quad
-// (the block's amax is a max, exact in any order), its two IEEE divisions done once for eight
-// values.  fa / fb: the finite flags of the two quads (a quad with a NaN or an infinity keeps
-// q = 0); pa / pb: their quants as bytes of one dword each.
-__device__ __forceinline__ void q8_oct(const float (&va)[4], const float (&vb)[4], float& d, int (&qa)[4],
-                                       int (&qb)[4], int& fa, int& fb, uint32_t& pa, uint32_t& pb) {
-    fa = finite_bits(va[0]) & finite_bits(va[1]) & finite_bits(va[2]) & finite_bits(va[3]);
-    fb = finite_bits(vb[0]) & finite_bits(vb[1]) & finite_bits(vb[2]) & finite_bits(vb[3]);
-    float amax = fmaxf(fmaxf(fmaxf(fabsf(va[0]), fabsf(va[1])), fmaxf(fabsf(va[2]), fabsf(va[3]))),
-                       fmaxf(fmaxf(fabsf(vb[0]), fabsf(vb[1])), fmaxf(fabsf(vb[2]), fabsf(vb[3]))));
-    amax = group_max<4>(amax);
+// 32-value block whose four lanes (k = 0..3) call this together: for a block of finite values
+// the same d and quants as q8_quad (the block's amax is a max, exact in any order; its two
+// divisions done once for eight values).  The amax is taken over the bit patterns of |v| as
+// unsigned integers, which order exactly as the floats for finite values and infinity, with
+// every NaN above +inf: the block is finite exactly when that maximum is below +inf's bits,
+// and fin = 0 otherwise.  A non-finite block's quants are unspecified (every GEMV that uses
+// this turns such a row of y into NaN).  pa / pb: the two quads' quants as bytes of one dword.
+__device__ __forceinline__ void q8_oct(const float (&va)[4], const float (&vb)[4], float& d, int& fin, uint32_t& pa,
+                                       uint32_t& pb) {
+    constexpr uint32_t kAbs = 0x7fffffffu;
+    const uint32_t ma = max(max(__float_as_uint(va[0]) & kAbs, __float_as_uint(va[1]) & kAbs),
+                            max(__float_as_uint(va[2]) & kAbs, __float_as_uint(va[3]) & kAbs));
+    const uint32_t mb = max(max(__float_as_uint(vb[0]) & kAbs, __float_as_uint(vb[1]) & kAbs),
+                            max(__float_as_uint(vb[2]) & kAbs, __float_as_uint(vb[3]) & kAbs));
+    uint32_t m = max(ma, mb);
+    m = max(m, static_cast<uint32_t>(dpp_i<kDppQuadXor1>(static_cast<int>(m))));
+    m = max(m, static_cast<uint32_t>(dpp_i<kDppQuadXor2>(static_cast<int>(m))));
+    fin = m < 0x7f800000u ? 1 : 0;
     float id;
-    q8_scale(amax, d, id);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        qa[i] = fa ? round_half_away(va[i] * id) : 0;
-        qb[i] = fb ? round_half_away(vb[i] * id) : 0;
-    }
-    pa = (static_cast<uint32_t>(qa[0]) & 0xffu) | ((static_cast<uint32_t>(qa[1]) & 0xffu) << 8) |
-         ((static_cast<uint32_t>(qa[2]) & 0xffu) << 16) | (static_cast<uint32_t>(qa[3]) << 24);
-    pb = (static_cast<uint32_t>(qb[0]) & 0xffu) | ((static_cast<uint32_t>(qb[1]) & 0xffu) << 8) |
-         ((static_cast<uint32_t>(qb[2]) & 0xffu) << 16) | (static_cast<uint32_t>(qb[3]) << 24);
+    q8_scale(__uint_as_float(m), d, id);
+    pa = pack_low_bytes(round_half_away(va[0] * id), round_half_away(va[1] * id), round_half_away(va[2] * id),
+                        round_half_away(va[3] * id));
+    pb = pack_low_bytes(round_half_away(vb[0] * id), round_half_away(vb[1] * id), round_half_away(vb[2] * id),
+                        round_half_away(vb[3] * id));
 }
 
 // The reference's vectorised exp (simd_math.hpp:63-117, used by its SiLU and softmax): clamp

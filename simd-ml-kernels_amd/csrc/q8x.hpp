@@ -53,18 +53,19 @@ __device__ __forceinline__ void quantize_quad(const float (&v)[4], int m, int kq
 }
 
 // Two quads of x, k and k + 4 of block b (four consecutive threads hold the block, k = 0..3),
-// into the LDS quants, biases and scale as quantize_quad stores them.  The reference lane k of
-// the Q4_0 order owns exactly these two quads, so its chain bias needs no other lane.
+// into the LDS quants, biases and scale as quantize_quad stores them (for a block with a NaN or
+// an infinity: bad[m] = 1 and the block's quants unspecified).  The reference lane k of the
+// Q4_0 order owns exactly these two quads, so its chain bias needs no other lane.
 template <bool kPlanes, bool kBias, bool kChainBias = false>
 __device__ __forceinline__ void quantize_oct(const float (&va)[4], const float (&vb)[4], int m, int b, int k, int K,
                                              uint32_t* lds_q, int* lds_bias, float* lds_dx, int* bad,
                                              bool live = true) {
     const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
     float d;
-    int qa[4], qb[4], fa, fb;
+    int fin;
     uint32_t pa, pb;
-    q8_oct(va, vb, d, qa, qb, fa, fb, pa, pb);
-    const int s8 = qa[0] + qa[1] + qa[2] + qa[3] + qb[0] + qb[1] + qb[2] + qb[3];
+    q8_oct(va, vb, d, fin, pa, pb);
+    const int s8 = dot4(pa, 0x01010101u, dot4(pb, 0x01010101u, 0));  // the eight signed quants
     const int s = kBias ? group_sum_int<4>(s8) : 0;
     if (live) {
         lds_q[m * quads + x_dword_index<kPlanes>(b, k, pairs)] = pa;
@@ -72,7 +73,7 @@ __device__ __forceinline__ void quantize_oct(const float (&va)[4], const float (
         if (kChainBias) lds_bias[(m * nb + b) * 4 + k] = -8 * s8;
         if (kBias && k == 0) lds_bias[m * nb + b] = -8 * s;
         if (k == 0) lds_dx[m * nb + b] = d;
-        if (!(fa & fb)) bad[m] = 1;
+        if (!fin) bad[m] = 1;
     }
 }
 
