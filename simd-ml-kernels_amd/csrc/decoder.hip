@@ -212,6 +212,66 @@ __device__ __forceinline__ float position_score(const float* __restrict__ qs, co
     return scale * v[0];
 }
 
+// Eight positions of the p.V chain: p[t .. t + 7] (16-byte aligned) and v[t * hd] .. v[(t + 7) * hd].
+struct PvBatch {
+    float4 a, b;
+    float w[8];
+};
+template <int HD>
+__device__ __forceinline__ void pv_load(const float* __restrict__ p, const float* __restrict__ v, int hd_arg, int t,
+                                        PvBatch& o) {
+    const int hd = HD > 0 ? HD : hd_arg;
+    const float4* p4 = reinterpret_cast<const float4*>(p + t);
+    o.a = p4[0];
+    o.b = p4[1];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o.w[i] = v[(t + i) * hd];
+}
+__device__ __forceinline__ float pv_fma(const PvBatch& o, float acc) {
+    acc = fmaf(o.a.x, o.w[0], acc);
+    acc = fmaf(o.a.y, o.w[1], acc);
+    acc = fmaf(o.a.z, o.w[2], acc);
+    acc = fmaf(o.a.w, o.w[3], acc);
+    acc = fmaf(o.b.x, o.w[4], acc);
+    acc = fmaf(o.b.y, o.w[5], acc);
+    acc = fmaf(o.b.z, o.w[6], acc);
+    return fmaf(o.b.w, o.w[7], acc);
+}
+
+// acc after the fused chain acc = fma(p[t], v[t * hd], acc) for t = 0 .. n - 1 in order (p 16-byte
+// aligned).  Eight positions a batch in two register sets used in turn: the reads of the next
+// batch are issued before the FMAs of the current one and stay in flight across the loop, so
+// that the chain waits on LDS once per batch at most, not once per position.
+template <int HD>
+__device__ __forceinline__ float pv_chain(const float* __restrict__ p, const float* __restrict__ v, int n, int hd_arg,
+                                          float acc) {
+    const int hd = HD > 0 ? HD : hd_arg;
+    const int n8 = n & ~7;
+    if (n8 > 0) {
+        PvBatch s0, s1;
+        pv_load<HD>(p, v, hd, 0, s0);
+        int t = 8;  // s0 holds batch t - 8
+        for (; t + 8 < n8; t += 16) {
+            pv_load<HD>(p, v, hd, t, s1);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv_fma(s0, acc);
+            pv_load<HD>(p, v, hd, t + 8, s0);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv_fma(s1, acc);
+        }
+        if (t < n8) {  // t == n8 - 8: one batch left besides s0
+            pv_load<HD>(p, v, hd, t, s1);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = pv_fma(s0, acc);
+            acc = pv_fma(s1, acc);
+        } else {
+            acc = pv_fma(s0, acc);
+        }
+    }
+    for (int t = n8; t < n; ++t) acc = fmaf(p[t], v[t * hd], acc);
+    return acc;
+}
+
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __restrict__ qkv,
                                                                  const float* __restrict__ cos_tab,
@@ -223,7 +283,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
                                                                  float* __restrict__ out, int pos_first,
                                                                  int qkv_stride, int out_stride) {
     constexpr int kWaves = kAttnThreads / kWave;
-    extern __shared__ float sc[];  // T scores then exponentials; then the K and V tiles
+    extern __shared__ __align__(16) float sc[];  // T scores, exponentials, then p; then the K and V tiles
     __shared__ __align__(16) float qs[kHeadMax];
     __shared__ float ks[kHeadMax], vs[kHeadMax];
     __shared__ float red_f[kWaves];
@@ -379,9 +439,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     }
     __syncthreads();
 
-    // out[d] = one fused chain over the positions in order of p[t] * V[t][d], p[t] = e[t] / sum
-    // as the product e[t] * (1 / sum) (NaN for a row with a NaN or infinite score).
+    // p[t] = e[t] / sum as the product e[t] * (1 / sum) (NaN for a row with a NaN or infinite
+    // score), in place, by every thread.
     const float inv = nan_row ? __builtin_nanf("") : inv_s;  // NaN * e = NaN for every position
+    for (int t = tid; t < T; t += kAttnThreads) sc[t] = sc[t] * inv;
+    __syncthreads();
+
+    // out[d] = one fused chain over the positions in order of p[t] * V[t][d].
     float acc = 0.0f;
     const int d = tid;
     for (int t0 = 0; t0 < T; t0 += tile) {
@@ -396,10 +460,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
                 for (int e = tid; e < hd; e += kAttnThreads) vtile[(pos - t0) * hd + e] = vs[e];
             __syncthreads();
         }
-        if (d < hd) {
-#pragma unroll 8
-            for (int t = 0; t < tn; ++t) acc = fmaf(sc[t0 + t] * inv, vtile[t * hd + d], acc);
-        }
+        if (d < hd) acc = pv_chain<HD>(sc + t0, vtile + d, tn, hd, acc);
     }
     if (d < hd) out[static_cast<size_t>(head) * hd + d] = acc;
 }
@@ -408,7 +469,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
 // leaves beside the scores (at least 16).
 int attention_tile(int cap, int hd) {
     const size_t left = kAttnLdsBudget / 4 - static_cast<size_t>((cap + 3) & ~3) - 4;  // 4: the spare slot
-    const int fit = static_cast<int>(left / static_cast<size_t>(k_stride(hd) + hd));
+    // (a multiple of 8, so that every round's p starts 16-byte aligned)
+    const int fit = static_cast<int>(left / static_cast<size_t>(k_stride(hd) + hd)) & ~7;
     return std::max(16, std::min({kMaxTile, cap, fit}));
 }
 size_t attention_lds(int cap, int hd) {
