@@ -212,55 +212,114 @@ __device__ __forceinline__ float position_score(const float* __restrict__ qs, co
     return scale * v[0];
 }
 
-// Eight positions of the p.V chain: p[t .. t + 7] (16-byte aligned) and v[t * hd] .. v[(t + 7) * hd].
+// v of lane l as a wave-uniform value.
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(v));
+    const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(u & 0xffffffffu), l));
+    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), l));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
+// 0.0 + f[0] + f[8] + ... + f[8 (n - 1)], in double, in order.  The reads in batches of eight in
+// two register sets used in turn (each batch's reads issued before the previous batch's adds);
+// the last n % 8 values, read with clamped indices, are issued first of all.
+template <bool kClamp>
+__device__ __forceinline__ void dsum_load(const float* __restrict__ f, int n, int i0, float (&r)[8]) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) r[u] = f[8 * (kClamp ? min(i0 + u, n - 1) : i0 + u)];
+}
+__device__ __forceinline__ double dsum_add(const float (&r)[8], double acc, int live = 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+        if (u < live) acc = acc + static_cast<double>(r[u]);
+    return acc;
+}
+__device__ __forceinline__ double strided_dsum(const float* __restrict__ f, int n) {
+    double acc = 0.0;
+    const int nb = n >> 3, rem = n & 7;
+    if (n == 0) return acc;
+    // Both issued unconditionally, with no branch between them (the first batch's reads stay
+    // among the values that the caller's f holds).
+    float tl[8], a[8], b[8];
+    dsum_load<true>(f, n, 8 * nb, tl);
+    dsum_load<true>(f, n, 0, a);
+    __builtin_amdgcn_sched_barrier(0);
+    if (nb > 0) {
+        int k = 1;  // a holds batch k - 1
+        for (; k + 1 < nb; k += 2) {
+            dsum_load<false>(f, n, 8 * k, b);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = dsum_add(a, acc);
+            dsum_load<false>(f, n, 8 * k + 8, a);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = dsum_add(b, acc);
+        }
+        if (k < nb) {
+            dsum_load<false>(f, n, 8 * k, b);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = dsum_add(a, acc);
+            acc = dsum_add(b, acc);
+        } else {
+            acc = dsum_add(a, acc);
+        }
+    }
+    return rem ? dsum_add(tl, acc, rem) : acc;
+}
+
+// Eight positions of the p.V chain from position t: p[t .. t + 7] (16-byte aligned; the reads may
+// pass the n positions, into LDS that the kernel owns) and rows t .. t + 7 of v (kClamp: clamped
+// to row n - 1).
 struct PvBatch {
     float4 a, b;
     float w[8];
 };
-template <int HD>
-__device__ __forceinline__ void pv_load(const float* __restrict__ p, const float* __restrict__ v, int hd_arg, int t,
-                                        PvBatch& o) {
+template <int HD, bool kClamp>
+__device__ __forceinline__ void pv_load(const float* __restrict__ p, const float* __restrict__ v, int hd_arg, int n,
+                                        int t, PvBatch& o) {
     const int hd = HD > 0 ? HD : hd_arg;
     const float4* p4 = reinterpret_cast<const float4*>(p + t);
     o.a = p4[0];
     o.b = p4[1];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o.w[i] = v[(t + i) * hd];
+    for (int i = 0; i < 8; ++i) o.w[i] = v[(kClamp ? min(t + i, n - 1) : t + i) * hd];
 }
-__device__ __forceinline__ float pv_fma(const PvBatch& o, float acc) {
-    acc = fmaf(o.a.x, o.w[0], acc);
-    acc = fmaf(o.a.y, o.w[1], acc);
-    acc = fmaf(o.a.z, o.w[2], acc);
-    acc = fmaf(o.a.w, o.w[3], acc);
-    acc = fmaf(o.b.x, o.w[4], acc);
-    acc = fmaf(o.b.y, o.w[5], acc);
-    acc = fmaf(o.b.z, o.w[6], acc);
-    return fmaf(o.b.w, o.w[7], acc);
+// The batch's first `live` positions (all eight by default) into the chain, in order.
+__device__ __forceinline__ float pv_fma(const PvBatch& o, float acc, int live = 8) {
+    const float pp[8] = {o.a.x, o.a.y, o.a.z, o.a.w, o.b.x, o.b.y, o.b.z, o.b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        if (i < live) acc = fmaf(pp[i], o.w[i], acc);
+    return acc;
 }
 
 // acc after the fused chain acc = fma(p[t], v[t * hd], acc) for t = 0 .. n - 1 in order (p 16-byte
-// aligned).  Eight positions a batch in two register sets used in turn: the reads of the next
-// batch are issued before the FMAs of the current one and stay in flight across the loop, so
-// that the chain waits on LDS once per batch at most, not once per position.
+// aligned, readable to 8 floats past n rounded down to 8).  Eight positions a batch in two
+// register sets used in turn: the reads of the next batch are issued before the FMAs of the
+// current one and stay in flight across the loop, so that the chain waits on LDS once per batch
+// at most, not once per position.  The last n % 8 positions are read first of all.
 template <int HD>
 __device__ __forceinline__ float pv_chain(const float* __restrict__ p, const float* __restrict__ v, int n, int hd_arg,
                                           float acc) {
     const int hd = HD > 0 ? HD : hd_arg;
-    const int n8 = n & ~7;
-    if (n8 > 0) {
-        PvBatch s0, s1;
-        pv_load<HD>(p, v, hd, 0, s0);
-        int t = 8;  // s0 holds batch t - 8
-        for (; t + 8 < n8; t += 16) {
-            pv_load<HD>(p, v, hd, t, s1);
+    const int nb = n >> 3, rem = n & 7;
+    // Both issued unconditionally, with no branch between them (n >= 1; with n < 8 the first
+    // batch reads rows 0 .. 7 of a tile of at least 16 rows and is not used).
+    PvBatch tl, s0, s1;
+    pv_load<HD, true>(p, v, hd, n, 8 * nb, tl);
+    pv_load<HD, false>(p, v, hd, n, 0, s0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (nb > 0) {
+        int b = 1;  // s0 holds batch b - 1
+        for (; b + 1 < nb; b += 2) {
+            pv_load<HD, false>(p, v, hd, n, 8 * b, s1);
             __builtin_amdgcn_sched_barrier(0);
             acc = pv_fma(s0, acc);
-            pv_load<HD>(p, v, hd, t + 8, s0);
+            pv_load<HD, false>(p, v, hd, n, 8 * b + 8, s0);
             __builtin_amdgcn_sched_barrier(0);
             acc = pv_fma(s1, acc);
         }
-        if (t < n8) {  // t == n8 - 8: one batch left besides s0
-            pv_load<HD>(p, v, hd, t, s1);
+        if (b < nb) {
+            pv_load<HD, false>(p, v, hd, n, 8 * b, s1);
             __builtin_amdgcn_sched_barrier(0);
             acc = pv_fma(s0, acc);
             acc = pv_fma(s1, acc);
@@ -268,8 +327,7 @@ __device__ __forceinline__ float pv_chain(const float* __restrict__ p, const flo
             acc = pv_fma(s0, acc);
         }
     }
-    for (int t = n8; t < n; ++t) acc = fmaf(p[t], v[t * hd], acc);
-    return acc;
+    return rem ? pv_fma(tl, acc, rem) : acc;
 }
 
 template <int HD>
@@ -403,39 +461,32 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
         nonfinite |= red_i[w];
     }
     const bool nan_row = nonfinite || __float_as_uint(mx) == 0xff800000u;
+    // The last T % 8 positions take the double exp, in the last eight threads, beside the
+    // others' SIMD exp (the last wave has no other position unless T > kAttnThreads - 64).
     const int n8 = T - T % 8;
-    for (int t = tid; t < T; t += kAttnThreads) {
-        const float dd = sc[t] - mx;
-        if (t < n8) {
-            sc[t] = exp_cody_waite(dd);
-        } else {
-            const double e = exp(static_cast<double>(dd));
-            tail_e[t - n8] = e;
-            sc[t] = static_cast<float>(e);
+    for (int t = tid; t < n8; t += kAttnThreads) sc[t] = exp_cody_waite(sc[t] - mx);
+    if (tid >= kAttnThreads - 8) {
+        const int j = tid - (kAttnThreads - 8);
+        if (j < T - n8) {
+            const double e = exp(static_cast<double>(sc[n8 + j] - mx));
+            tail_e[j] = e;
+            sc[n8 + j] = static_cast<float>(e);
         }
     }
     __syncthreads();
     if (wave == 0) {
-        double acc = 0.0;
-        if (lane < 8) {
-            int t = lane;
-            for (; t + 56 < n8; t += 64) {  // eight reads issued before the eight adds
-                float e[8];
+        const double acc = lane < 8 ? strided_dsum(sc + lane, n8 / 8) : 0.0;
+        double tail[7];  // read before the lane sums are gathered (entries past T % 8 unused)
 #pragma unroll
-                for (int u = 0; u < 8; ++u) e[u] = sc[t + 8 * u];
+        for (int j = 0; j < 7; ++j) tail[j] = tail_e[j];
+        double tsum = readlane_d(acc, 0);
 #pragma unroll
-                for (int u = 0; u < 8; ++u) acc = acc + static_cast<double>(e[u]);
-            }
-            for (; t < n8; t += 8) acc = acc + static_cast<double>(sc[t]);
-        }
-        double tsum = __shfl(acc, 0, kWave);
+        for (int k = 1; k < 8; ++k) tsum = tsum + readlane_d(acc, k);
+        double sum = 0.0 + tsum;
 #pragma unroll
-        for (int k = 1; k < 8; ++k) tsum = tsum + __shfl(acc, k, kWave);
-        if (lane == 0) {
-            double sum = 0.0 + tsum;
-            for (int t = 0; t < T - n8; ++t) sum = sum + tail_e[t];
-            inv_s = static_cast<float>(1.0 / sum);
-        }
+        for (int j = 0; j < 7; ++j)
+            if (j < T - n8) sum = sum + tail[j];
+        if (lane == 0) inv_s = static_cast<float>(1.0 / sum);
     }
     __syncthreads();
 
