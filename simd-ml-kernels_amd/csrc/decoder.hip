@@ -868,11 +868,18 @@ hipError_t enqueue_step(Model& md, bool with_logits, Marks* mk = nullptr, bool e
         return hipGetLastError();
     }
     SMK_MARK(kLmHead);
-    // The final RMSNorm as a kernel of its own, then the plain lm_head product: a plain Q4_0
-    // product of this many rows takes the K-chunk tiled kernel, which the fused-norm form cannot
-    // (same bits either way).
-    if (const hipError_t e = rms_norm(md.x, md.out_norm, md.h, 1, c.hidden, c.rms_eps, s); e != hipSuccess) return e;
-    if (const hipError_t e = gemv(md.head, md.h, md.logits, false, s); e != hipSuccess) return e;
+    if (md.fuse_norm && md.head.type == kGgmlQ4_0 && c.hidden == 2048) {
+        // One launch: the lm_head's tiled kernel normalizes x in its prologue (width 2048).
+        if (const hipError_t e = gemv_normed(md, md.head, md.x, md.out_norm, md.h, md.logits, false); e != hipSuccess)
+            return e;
+    } else {
+        // The final RMSNorm as a kernel of its own, then the plain lm_head product: a plain Q4_0
+        // product of this many rows takes the K-chunk tiled kernel, which the fused-norm form
+        // takes only at width 2048 (same bits either way).
+        if (const hipError_t e = rms_norm(md.x, md.out_norm, md.h, 1, c.hidden, c.rms_eps, s); e != hipSuccess)
+            return e;
+        if (const hipError_t e = gemv(md.head, md.h, md.logits, false, s); e != hipSuccess) return e;
+    }
     SMK_MARK(kArgmax);
     hipLaunchKernelGGL(argmax_part_kernel, dim3(kArgmaxParts), dim3(kArgmaxThreads), 0, s, md.logits, c.vocab,
                        md.part_v, md.part_i);

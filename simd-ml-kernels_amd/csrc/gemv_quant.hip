@@ -798,11 +798,16 @@ __host__ __device__ __forceinline__ int tiled_x_words(int K) {
 // TF: tiles in flight (register buffers); PQ: octs of x a thread loads before the weights;
 // XR: chunks per row whose x data the dot lanes hold in registers (1 or 2: the row has exactly
 // that many chunks; TF a multiple of XR), 0: read from LDS each tile.
-template <int TF, int PQ, int XR>
+// kNorm: x is replaced by RMSNorm(x) * norm_w (K = 2048, one chunk: the mean of squares by one
+// wave from registers, as the row-group kernel's prologue; the same quantized image as the
+// separate RMSNorm kernel followed by the plain product).
+template <int TF, int PQ, int XR, bool kNorm>
 __global__ __launch_bounds__(tiled::kThreads) void gemv_q4_tiled_kernel(int N, int K, const float* __restrict__ x,
                                                                         const uint8_t* __restrict__ W,
                                                                         float* __restrict__ y, int rows_per_wg,
-                                                                        int accumulate, int silu_pairs) {
+                                                                        int accumulate, int silu_pairs,
+                                                                        const float* __restrict__ norm_w,
+                                                                        double norm_eps) {
     constexpr int kThreads = tiled::kThreads, kRows = tiled::kRows, kBlocks = tiled::kBlocks;
     constexpr int kRowBytes = tiled::kRowBytes, kPiecesPerRow = tiled::kPiecesPerRow, kPieces = tiled::kPieces;
     constexpr int kPiecesPerThread = tiled::kPiecesPerThread, kStride = tiled::kStride;
@@ -953,17 +958,48 @@ __global__ __launch_bounds__(tiled::kThreads) void gemv_q4_tiled_kernel(int N, i
 
     // x first (its own loads, every wave's ahead of any weight load), then the first TF tiles,
     // then x is quantized while they are in flight.
-    XPreload<kThreads, PQ, 1> xpre;
-    xpre.load(x, K, 1, K);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
     Slot ring[TF];
+    if constexpr (kNorm) {
+        static_assert(XR == 1, "the fused norm: K = 2048, one chunk");
+        __shared__ float norm_scale;
+        const int quads = K >> 2;  // 512 <= kThreads: one quad a thread
+        const int qd = tid < quads ? tid : 0;
+        const float4 xq = reinterpret_cast<const float4*>(x)[qd];
+        const float4 wq = reinterpret_cast<const float4*>(norm_w)[qd];
+        float2 xw[16];
+        if (wave == 0) {
 #pragma unroll
-    for (int s = 0; s < TF; ++s) load_tile(s, ring[s]);
-    __builtin_amdgcn_sched_barrier(0);
-    xpre.template quantize<true, false, true>(x, K, 1, K, lds_q, lds_cb, lds_dx, bad);
+            for (int j = 0; j < 16; ++j) xw[j] = *reinterpret_cast<const float2*>(x + wave_sumsq_index(j));
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < TF; ++s) load_tile(s, ring[s]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (wave == 0) {
+            const float total = wave_sumsq_2048(xw);
+            const float var = static_cast<float>(static_cast<double>(total) / static_cast<double>(K));
+            if (lane == 0) norm_scale = static_cast<float>(1.0 / sqrt(static_cast<double>(var) + norm_eps));
+        }
+        lds_barrier();
+        const float scale = norm_scale;
+        const float h[4] = {wq.x * (xq.x * scale), wq.y * (xq.y * scale), wq.z * (xq.z * scale),
+                            wq.w * (xq.w * scale)};
+        quantize_quad<true, false, true>(h, 0, qd, K, lds_q, lds_cb, lds_dx, bad, tid < quads);
+    } else {
+        XPreload<kThreads, PQ, 1> xpre;
+        xpre.load(x, K, 1, K);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < TF; ++s) load_tile(s, ring[s]);
+        __builtin_amdgcn_sched_barrier(0);
+        xpre.template quantize<true, false, true>(x, K, 1, K, lds_q, lds_cb, lds_dx, bad);
+    }
     lds_barrier();
     // The dot lanes' x data, for the chunks a row has (held in registers when XR > 0).
     constexpr int kXr = XR > 0 ? XR : 1;
@@ -1378,14 +1414,14 @@ bool tiled_ok(int K, const uint8_t* W, int rows_per_wg, int acc) {
            tiled_lds_bytes(K, rows_per_wg, acc) <= 150 * 1024;
 }
 
-template <int TF, int PQ, int XR>
+template <int TF, int PQ, int XR, bool kNorm = false>
 hipError_t launch_tiled_kernel(int N, int K, const float* x, const uint8_t* W, float* y, int rpw, int acc, int silu,
-                               hipStream_t stream) {
+                               hipStream_t stream, const float* norm_w = nullptr, double norm_eps = 0.0) {
     const size_t lds = tiled_lds_bytes(K, rpw, acc);
-    if (const hipError_t e = allow_lds(gemv_q4_tiled_kernel<TF, PQ, XR>, lds); e != hipSuccess) return e;
+    if (const hipError_t e = allow_lds(gemv_q4_tiled_kernel<TF, PQ, XR, kNorm>, lds); e != hipSuccess) return e;
     const int grid = (N + rpw - 1) / rpw;
-    hipLaunchKernelGGL((gemv_q4_tiled_kernel<TF, PQ, XR>), dim3(grid), dim3(tiled::kThreads), lds, stream, N, K, x, W,
-                       y, rpw, acc, silu);
+    hipLaunchKernelGGL((gemv_q4_tiled_kernel<TF, PQ, XR, kNorm>), dim3(grid), dim3(tiled::kThreads), lds, stream, N, K,
+                       x, W, y, rpw, acc, silu, norm_w, norm_eps);
     return hipGetLastError();
 }
 
@@ -1492,8 +1528,11 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
     // Short rows and few rows keep the row-group kernel (8192x2048 5.65 / 4.38, 14336x4096 11.0 /
     // 10.4, 2048x8192 8.15 / 6.25): its one or two groups need fewer barriers.
     const bool tiled_pays = g_q4_tiles > 0 || K >= 12288 || rpw >= 256;
-    if (mt == 1 && !nrm.w && !(t && (t->lanes_per_row || t->threads)) && tiled_pays && tiled_ok(K, W, rpw, acc) &&
-        !(nrm.silu_pairs && (rpw & 1))) {
+    // The fused norm in the tiled kernel: K = 2048 (one chunk, the one-wave mean of squares).
+    const bool tiled_norm = nrm.w && K == 2048 && nrm.depth == 4 && !acc && !nrm.silu_pairs;
+    if (mt == 1 && (!nrm.w || tiled_norm) && !(t && (t->lanes_per_row || t->threads)) && tiled_pays &&
+        tiled_ok(K, W, rpw, acc) && !(nrm.silu_pairs && (rpw & 1))) {
+        if (nrm.w) return launch_tiled_kernel<2, 1, 1, true>(N, K, x, W, y, rpw, 0, 0, stream, nrm.w, nrm.eps);
         return launch_tiled(N, K, x, W, y, rpw, acc, nrm.silu_pairs, stream);
     }
     if (mt == 1) {
