@@ -417,7 +417,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     __syncthreads();
 
     // Scores, `tile` positions a round (one thread a position); rounds after the first restage
-    // the K tile, position pos from ks.
+    // the K tile, position pos from ks.  Each thread keeps the maximum of the scores it writes
+    // (and whether one is NaN or +inf) for the softmax.
+    float mx = -__builtin_inff();
+    int nonfinite = 0;
     for (int t0 = 0; t0 < T; t0 += tile) {
         const int tn = min(tile, T - t0);
         if (t0 > 0) {
@@ -430,22 +433,19 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
                 for (int d = tid; d < hd; d += kAttnThreads) ktile[(pos - t0) * kst + d] = ks[d];
             __syncthreads();
         }
-        for (int t = tid; t < tn; t += kAttnThreads) sc[t0 + t] = position_score<HD>(qs, ktile + t * kst, hd, scale);
+        for (int t = tid; t < tn; t += kAttnThreads) {
+            const float v = position_score<HD>(qs, ktile + t * kst, hd, scale);
+            sc[t0 + t] = v;
+            const uint32_t u = __float_as_uint(v);
+            nonfinite |= (u & 0x7fffffffu) > 0x7f800000u || u == 0x7f800000u;
+            mx = fmaxf(mx, v);
+        }
     }
-    __syncthreads();
 
-    // Softmax over the T scores: the maximum (and whether any score is NaN or infinite), the
-    // exponentials (the SIMD exp on full groups of 8, double exp on the last T % 8), then the
-    // eight running double sums of the groups of 8 (lane j: positions j, j+8, ... in order),
-    // added in lane order, then the tail's doubles, and 1 / sum.
-    float mx = -__builtin_inff();
-    int nonfinite = 0;
-    for (int t = tid; t < T; t += kAttnThreads) {
-        const float v = sc[t];
-        const uint32_t u = __float_as_uint(v);
-        nonfinite |= (u & 0x7fffffffu) > 0x7f800000u || u == 0x7f800000u;
-        mx = fmaxf(mx, v);
-    }
+    // Softmax over the T scores: the maximum (and whether any score is NaN or infinite; the
+    // waves' partial maxima combined), the exponentials (the SIMD exp on full groups of 8, double
+    // exp on the last T % 8), then the eight running double sums of the groups of 8 (lane j:
+    // positions j, j+8, ... in order), added in lane order, then the tail's doubles, and 1 / sum.
     mx = group_max<kWave>(mx);
     nonfinite = group_sum_int<kWave>(nonfinite);
     if (lane == 0) {
