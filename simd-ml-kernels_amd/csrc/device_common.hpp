@@ -174,6 +174,24 @@ __device__ __forceinline__ uint32_t pack_low_bytes(int q0, int q1, int q2, int q
     return lo | hi;
 }
 
+// q8_quad for the GEMV kernels: the same d and quants for a block of finite values (the amax as
+// an unsigned maximum over |v|'s bit patterns, as q8_oct), fin = 0 for the whole block when any
+// of its values is a NaN or an infinity, whose quants are then unspecified (the GEMV's row of y
+// is NaN).  Returns the four quants as bytes of one dword, value 4k in the low byte.
+__device__ __forceinline__ uint32_t q8_quad_gemv(const float (&v)[4], float& d, int& fin) {
+    constexpr uint32_t kAbs = 0x7fffffffu;
+    uint32_t m = max(max(__float_as_uint(v[0]) & kAbs, __float_as_uint(v[1]) & kAbs),
+                     max(__float_as_uint(v[2]) & kAbs, __float_as_uint(v[3]) & kAbs));
+    m = max(m, static_cast<uint32_t>(dpp_i<kDppQuadXor1>(static_cast<int>(m))));
+    m = max(m, static_cast<uint32_t>(dpp_i<kDppQuadXor2>(static_cast<int>(m))));
+    m = max(m, static_cast<uint32_t>(dpp_i<kDppHalfMirror>(static_cast<int>(m))));
+    fin = m < 0x7f800000u ? 1 : 0;
+    float id;
+    q8_scale(__uint_as_float(m), d, id);
+    return pack_low_bytes(round_half_away(v[0] * id), round_half_away(v[1] * id), round_half_away(v[2] * id),
+                          round_half_away(v[3] * id));
+}
+
 // Q8 quants of two quads of x, k and k + 4 (values 4k..4k+3 and 16+4k..16+4k+3) of a
 // 32-value block whose four lanes (k = 0..3) call this together: for a block of finite values
 // the same d and quants as q8_quad (the block's amax is a max, exact in any order; its two

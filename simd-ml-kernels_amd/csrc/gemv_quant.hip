@@ -576,7 +576,7 @@ __global__ __launch_bounds__(NT) void gemv_q4_ordered_kernel(int M, int N, int K
             const bool live = qd < quads;
             const float h[4] = {wr[u].x * (xr[u].x * scale), wr[u].y * (xr[u].y * scale),
                                 wr[u].z * (xr[u].z * scale), wr[u].w * (xr[u].w * scale)};
-            quantize_quad<true, false, true>(h, 0, live ? qd : 0, K, lds_q, lds_cb, lds_dx, bad, live);
+            quantize_quad<true, false, true, true>(h, 0, live ? qd : 0, K, lds_q, lds_cb, lds_dx, bad, live);
         }
         lds_barrier();
     } else {
@@ -987,7 +987,7 @@ __global__ __launch_bounds__(tiled::kThreads) void gemv_q4_tiled_kernel(int N, i
         const float scale = norm_scale;
         const float h[4] = {wq.x * (xq.x * scale), wq.y * (xq.y * scale), wq.z * (xq.z * scale),
                             wq.w * (xq.w * scale)};
-        quantize_quad<true, false, true>(h, 0, qd, K, lds_q, lds_cb, lds_dx, bad, tid < quads);
+        quantize_quad<true, false, true, true>(h, 0, qd, K, lds_q, lds_cb, lds_dx, bad, tid < quads);
     } else {
         XPreload<kThreads, PQ, 1> xpre;
         xpre.load(x, K, 1, K);

@@ -29,20 +29,27 @@ __device__ __forceinline__ int x_dword_index(int b, int k, int pairs) {
 // kChainBias (reference-order Q4_0 kernel): lds_bias gets, per block b and reference lane k
 // (0..3), -8 * the sum of the quants of values {4k..4k+3} and {16+4k..16+4k+3}, at
 // [m * nb * 4 + 4 * b + k].
-template <bool kPlanes, bool kBias, bool kChainBias = false>
+// kGemv: q8_quad_gemv (a block with a NaN or an infinity: bad[m] = 1, its quants unspecified),
+// for the GEMV kernels whose row of y is then NaN; otherwise q8_quad, whose quants are exact for
+// every input (the standalone quantizer returns them).
+template <bool kPlanes, bool kBias, bool kChainBias = false, bool kGemv = false>
 __device__ __forceinline__ void quantize_quad(const float (&v)[4], int m, int kq, int K, uint32_t* lds_q,
                                               int* lds_bias, float* lds_dx, int* bad, bool live = true) {
     const int nb = K >> 5, pairs = nb >> 1, quads = K >> 2;
     const int b = kq >> 3, k = kq & 7;
     float d;
-    int q[4], fin;
-    const uint32_t packed = q8_quad(v, d, q, fin);
-    const int s = kBias ? group_sum_int<8>(q[0] + q[1] + q[2] + q[3]) : 0;
-    int chain = 0;
-    if constexpr (kChainBias) {
-        const int s4 = q[0] + q[1] + q[2] + q[3];
-        chain = -8 * (s4 + __shfl_xor(s4, 4, kWave));  // quads k and k + 4 of the block
+    int fin;
+    uint32_t packed;
+    if constexpr (kGemv) {
+        packed = q8_quad_gemv(v, d, fin);
+    } else {
+        int q[4];
+        packed = q8_quad(v, d, q, fin);
     }
+    const int s4 = dot4(packed, 0x01010101u, 0);  // the quad's four signed quants
+    const int s = kBias ? group_sum_int<8>(s4) : 0;
+    int chain = 0;
+    if constexpr (kChainBias) chain = -8 * (s4 + __shfl_xor(s4, 4, kWave));  // quads k and k + 4 of the block
     if (live) {
         lds_q[m * quads + x_dword_index<kPlanes>(b, k, pairs)] = packed;
         if (kChainBias && k < 4) lds_bias[(m * nb + b) * 4 + k] = chain;
