@@ -119,25 +119,31 @@ MID = dict(TINY, hidden_size=2048, intermediate_size=8192, num_attention_heads=3
            head_dim=64)
 
 
-def test_mid_model_logits_equal_reference_loop(tmp_path):
+@pytest.mark.parametrize("tiles", [0, 2])
+def test_mid_model_logits_equal_reference_loop(tmp_path, tiles):
     """Llama-3.2-1B layer widths (K = 2048 and 8192, the shapes of the fused GEMV launches) with
     two layers: logits bit-identical with the reference loop at every position, through the fused
-    RMSNorm prologues and the SiLU and residual epilogues."""
+    RMSNorm prologues and the SiLU and residual epilogues.  tiles = 2 forces the K-chunk tiled
+    kernel wherever it applies (smk_set_q4_tiles): the lm_head and q|k|v then take its fused-norm
+    prologue, o and down its plain form."""
+    from simd_ml_kernels import abi
     path, prompt = llama.write_synthetic_model(str(tmp_path), MID, seed=27, n_prompt=6, weight_type=gguf.Q4_0)
     c = lr.Cfg.from_config(MID)
     oprompt, W = lr.synthetic_model(c, 27, 6, lr.Q4_0)
     assert prompt == oprompt
     dec = lr.Decoder(c, W, lr.Q4_0, _oracle_kind())
     seq = prompt + [11, 222, 333]
+    abi.call("smk_set_q4_tiles", tiles)
     m = llama.Llama(str(tmp_path), gguf=path)
     try:
         m.reset(len(seq))
         dec.reset(len(seq))
         for i, t in enumerate(seq):
             np.testing.assert_array_equal(m.step(t).view(np.uint32), dec.step(t).view(np.uint32),
-                                          err_msg=f"position {i}")
+                                          err_msg=f"position {i}, tiles {tiles}")
     finally:
         m.close()
+        abi.call("smk_set_q4_tiles", 0)
 
 
 @pytest.mark.parametrize("wname,model,rows", [("q4_0", "tiny", 64), ("q4_0", "tiny", 3), ("q8_0", "tiny", 5),
