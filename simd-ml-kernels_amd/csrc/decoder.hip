@@ -461,11 +461,22 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
         nonfinite |= red_i[w];
     }
     const bool nan_row = nonfinite || __float_as_uint(mx) == 0xff800000u;
-    // The last T % 8 positions take the double exp, in the last eight threads, beside the
-    // others' SIMD exp (the last wave has no other position unless T > kAttnThreads - 64).
+    // The SIMD exp of the full groups of 8 by every thread; then, after a barrier, wave 0 runs the
+    // eight double sums of those while the last eight threads (another wave) take the double exp of
+    // the last T % 8 positions, which the sum needs only at its end; after a second barrier wave 0
+    // adds them and forms 1 / sum.
+    static_assert(kAttnThreads - 8 >= kWave, "the tail's threads are not in wave 0");
     const int n8 = T - T % 8;
     for (int t = tid; t < n8; t += kAttnThreads) sc[t] = exp_cody_waite(sc[t] - mx);
-    if (tid >= kAttnThreads - 8) {
+    __syncthreads();
+    double sum = 0.0;
+    if (wave == 0) {
+        const double acc = lane < 8 ? strided_dsum(sc + lane, n8 / 8) : 0.0;
+        double tsum = readlane_d(acc, 0);
+#pragma unroll
+        for (int k = 1; k < 8; ++k) tsum = tsum + readlane_d(acc, k);
+        sum = 0.0 + tsum;
+    } else if (tid >= kAttnThreads - 8) {
         const int j = tid - (kAttnThreads - 8);
         if (j < T - n8) {
             const double e = exp(static_cast<double>(sc[n8 + j] - mx));
@@ -475,14 +486,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* __
     }
     __syncthreads();
     if (wave == 0) {
-        const double acc = lane < 8 ? strided_dsum(sc + lane, n8 / 8) : 0.0;
-        double tail[7];  // read before the lane sums are gathered (entries past T % 8 unused)
+        double tail[7];  // entries past T % 8 unused
 #pragma unroll
         for (int j = 0; j < 7; ++j) tail[j] = tail_e[j];
-        double tsum = readlane_d(acc, 0);
-#pragma unroll
-        for (int k = 1; k < 8; ++k) tsum = tsum + readlane_d(acc, k);
-        double sum = 0.0 + tsum;
 #pragma unroll
         for (int j = 0; j < 7; ++j)
             if (j < T - n8) sum = sum + tail[j];
