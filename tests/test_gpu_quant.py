@@ -385,6 +385,43 @@ class TestBatchedMatrixCores:
             else:
                 np.testing.assert_array_equal(Y[m].view(np.uint32), ref.view(np.uint32), err_msg=f"row {m}")
 
+    @pytest.mark.parametrize("M", [3, 4, 8])
+    def test_nonfinite_rows_in_kernel_quantizer(self, M):
+        """A launch of 4 or 8 rows of x (the streaming kernel's smallest images): a row with a NaN
+        or an infinity is NaN; saturated and zero rows stay exact."""
+        N, K = 64, 2048
+        rng = np.random.default_rng(40 + M)
+        X = rng.standard_normal((M, K)).astype(np.float32)
+        X[0, 1000] = np.nan
+        X[M - 1, 5] = np.inf
+        X[1] = np.where(rng.standard_normal(K) > 0, 1.0, -1.0).astype(np.float32) * 1e30
+        if M > 3:
+            X[2] = 0.0
+        wq = o.quantize_q4_0(rng.standard_normal((N, K)).astype(np.float32))
+        Y = d_gemm("q4_0", X, wq, N, K)
+        for m in range(M):
+            ref = o.gemv_q4_0_simd(X[m], wq, N, K)
+            if m in (0, M - 1):
+                assert np.isnan(Y[m]).all() and np.isnan(ref).all()
+            else:
+                np.testing.assert_array_equal(Y[m].view(np.uint32), ref.view(np.uint32), err_msg=f"row {m}")
+
+    @pytest.mark.parametrize("M,ldx,xoff", [(4, 2049, 0), (8, 2048, 1), (8, 2052, 0), (5, 4100, 0)])
+    def test_row_stride_and_alignment_of_x(self, M, ldx, xoff):
+        """x rows at any stride (odd, padded) and any 4-byte alignment: every row equals the
+        reference order's."""
+        N, K = 96, 2048 if ldx < 4096 else 4096
+        rng = np.random.default_rng(ldx + xoff)
+        buf = rng.standard_normal(xoff + M * ldx).astype(np.float32)
+        X = np.stack([buf[xoff + m * ldx:xoff + m * ldx + K] for m in range(M)])
+        wq = o.quantize_q4_0(rng.standard_normal((N, K)).astype(np.float32))
+        xd, wd, yd = g.dev(buf), g.dev(wq), g.empty(4 * M * N)
+        g.call("smk_d_gemm_q4_0", M, N, K, g.ptr(xd, 4 * xoff), ldx, g.ptr(wd), g.ptr(yd), N, g.stream())
+        Y = g.host(yd, np.float32, M * N).reshape(M, N)
+        for m in range(M):
+            ref = o.gemv_q4_0_simd(X[m], wq, N, K)
+            np.testing.assert_array_equal(Y[m].view(np.uint32), ref.view(np.uint32), err_msg=f"row {m}")
+
     def test_two_byte_aligned_w_takes_gemv_path(self):
         M, N, K = 6, 40, 2048
         rng = np.random.default_rng(6)
