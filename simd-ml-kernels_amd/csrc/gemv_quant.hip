@@ -1528,8 +1528,9 @@ hipError_t gemv_q4_ordered(int M, int N, int K, const float* x, int ldx, const u
     }
     // The K-chunk tiled kernel where it measured faster on MI355X (graph-replayed, us, tiled /
     // row-group): long rows, 4096x14336 12.1 / 16.0; many rows a workgroup, 128256x4096 56.0 / 58.8.
-    // Short rows and few rows keep the row-group kernel (8192x2048 5.65 / 4.38, 14336x4096 11.0 /
-    // 10.4, 2048x8192 8.15 / 6.25): its one or two groups need fewer barriers.
+    // Short rows and few rows keep the row-group kernel (8192x2048 5.68 / 4.12, 16384x2048 7.55 /
+    // 5.67, 3072x2048 3.98 / 3.35, 2048x2048 3.94 / 3.22, 2048x8192 7.40 / 5.53, 14336x4096 11.0 /
+    // 10.4): its one or two groups need fewer barriers.
     const bool tiled_pays = g_q4_tiles > 0 || K >= 12288 || rpw >= 256;
     // The fused norm in the tiled kernel: K = 2048 (one chunk, the one-wave mean of squares).
     const bool tiled_norm = nrm.w && K == 2048 && nrm.depth == 4 && !acc && !nrm.silu_pairs;
